@@ -1,0 +1,710 @@
+// Fused quantize-dequantize kernels for MXFP/NVFP and HBQ block formats on gfx950.
+//
+// Layout: the input is viewed as [rows, cols] with blocks of `block` elements
+// along the last dimension (src/quantizer.py:67-146); a ragged last block is
+// zero padded.  Each lane owns 16 consecutive elements of one block (two
+// 16-byte loads for 16-bit types), so a block of B elements is handled by
+// B/16 adjacent lanes of one wavefront.  One pass reads x once and writes the
+// dequantized tensor, the element codes and the block scales.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "hbq_capi_internal.h"
+#include "hbq_numeric.h"
+
+namespace hbq {
+
+constexpr int kV = 16;          // elements per lane
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kThreads = 256;   // 4 wavefronts per workgroup
+
+template <class T>
+__device__ __forceinline__ void load16(const typename T::storage* __restrict__ p, float* v) {
+    if constexpr (sizeof(typename T::storage) == 2) {
+        const u32x4* q = reinterpret_cast<const u32x4*>(p);
+        u32x4 a = __builtin_nontemporal_load(q);
+        u32x4 b = __builtin_nontemporal_load(q + 1);
+        uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v[2 * i] = T::load((uint16_t)(w[i] & 0xffffu));
+            v[2 * i + 1] = T::load((uint16_t)(w[i] >> 16));
+        }
+    } else {
+        const f32x4* q = reinterpret_cast<const f32x4*>(p);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f32x4 a = __builtin_nontemporal_load(q + i);
+            v[4 * i] = a.x; v[4 * i + 1] = a.y; v[4 * i + 2] = a.z; v[4 * i + 3] = a.w;
+        }
+    }
+}
+
+template <class T>
+__device__ __forceinline__ void store16(typename T::storage* __restrict__ p, const float* v) {
+    if constexpr (sizeof(typename T::storage) == 2) {
+        uint32_t w[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = (uint32_t)T::store(v[2 * i]) | ((uint32_t)T::store(v[2 * i + 1]) << 16);
+        u32x4* q = reinterpret_cast<u32x4*>(p);
+        __builtin_nontemporal_store((u32x4){w[0], w[1], w[2], w[3]}, q);
+        __builtin_nontemporal_store((u32x4){w[4], w[5], w[6], w[7]}, q + 1);
+    } else {
+        f32x4* q = reinterpret_cast<f32x4*>(p);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_nontemporal_store((f32x4){v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]}, q + i);
+    }
+}
+
+// Codes of 16 consecutive elements starting at column c0 (a multiple of 16).
+// 4-bit formats pack two codes per byte (even column in the low nibble) with a
+// row stride of ceil(cols/2) bytes; wider formats use one byte per element.
+template <int M>
+__device__ __forceinline__ void store_codes(uint8_t* __restrict__ codes, int64_t row, int64_t cols, int64_t c0,
+                                            const uint32_t* c, bool RAGGED) {
+    if (codes == nullptr) return;
+    if constexpr (M == 1) {
+        const int64_t stride = (cols + 1) / 2;
+        uint8_t* p = codes + row * stride + c0 / 2;
+        if (!RAGGED) {
+            uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                w0 |= (c[i] & 0xfu) << (4 * i);
+                w1 |= (c[8 + i] & 0xfu) << (4 * i);
+            }
+            *reinterpret_cast<uint2*>(p) = make_uint2(w0, w1);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i += 2) {
+                if (c0 + i >= cols) break;
+                uint32_t hi = (c0 + i + 1 < cols) ? (c[i + 1] & 0xfu) : 0u;
+                p[i / 2] = (uint8_t)((c[i] & 0xfu) | (hi << 4));
+            }
+        }
+    } else {
+        uint8_t* p = codes + row * cols + c0;
+        if (!RAGGED) {
+            uint32_t w[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                w[i] = (c[4 * i] & 0xffu) | ((c[4 * i + 1] & 0xffu) << 8) | ((c[4 * i + 2] & 0xffu) << 16) |
+                       ((c[4 * i + 3] & 0xffu) << 24);
+            *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (c0 + i < cols) p[i] = (uint8_t)c[i];
+        }
+    }
+}
+
+// max of |x| bit patterns over a group of `lpb` lanes (NaN patterns order above +inf)
+__device__ __forceinline__ uint32_t group_max_bits(uint32_t v, int lpb) {
+    for (int off = 1; off < lpb; off <<= 1) {
+        uint32_t o = (uint32_t)__shfl_xor((int)v, off, 64);
+        v = v > o ? v : o;
+    }
+    return v;
+}
+
+struct Locate {
+    int64_t gb;     // global block index
+    int li;         // lane within the block
+    bool valid;
+    int64_t row, c0;
+};
+
+__device__ __forceinline__ Locate locate(int lpb_log2, int64_t nblk_row, int64_t nb, int block) {
+    Locate L;
+    int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    L.gb = t >> lpb_log2;
+    L.li = (int)(threadIdx.x & ((1 << lpb_log2) - 1));
+    L.valid = L.gb < nb;
+    int64_t g = L.valid ? L.gb : 0;
+    L.row = g / nblk_row;
+    L.c0 = (g - L.row * nblk_row) * block + (int64_t)L.li * kV;
+    return L;
+}
+
+template <class T>
+__device__ __forceinline__ void load_lane(const typename T::storage* __restrict__ x, const Locate& L, int64_t cols,
+                                          float* v, bool RAGGED) {
+    if (!RAGGED) {
+        if (L.valid) load16<T>(x + L.row * cols + L.c0, v);
+        else {
+#pragma unroll
+            for (int i = 0; i < kV; ++i) v[i] = 0.f;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < kV; ++i) {
+            int64_t c = L.c0 + i;
+            v[i] = (L.valid && c < cols) ? T::load(x[L.row * cols + c]) : 0.f;
+        }
+    }
+}
+
+template <class T>
+__device__ __forceinline__ void store_lane(typename T::storage* __restrict__ y, const Locate& L, int64_t cols,
+                                           const float* v, bool RAGGED) {
+    if (!L.valid) return;
+    if (!RAGGED) {
+        store16<T>(y + L.row * cols + L.c0, v);
+    } else {
+#pragma unroll
+        for (int i = 0; i < kV; ++i) {
+            int64_t c = L.c0 + i;
+            if (c < cols) y[L.row * cols + c] = T::store(v[i]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// MXFP / NVFP  (MXFPQuantizer.get_shared_scale + q, src/quantizer.py:481-539)
+// ---------------------------------------------------------------------------
+struct MxParams {
+    int pot;              // 1: power-of-two scale (sc_mbit == 0), 0: FP scale
+    int use_round;
+    float ele_emax;       // 2^(ebit-1)
+    float sc_emin, sc_emax;
+    float min_normal;     // added to an all-zero block before log2
+    float ele_maxnorm;    // element max normal (FP scale divisor)
+    ScaleFmt sf;          // FP scale format
+    int per_tensor;
+    float tscale;         // per-tensor scale, already rounded to T
+};
+
+template <class T>
+__device__ __forceinline__ float mx_shared_scale(float amax, const MxParams& p) {
+    if (p.pot) {
+        float v = T::round(amax + (amax == 0.f ? p.min_normal : 0.f));
+        float se;
+        if (v != v) se = v;
+        else if (v == __builtin_inff()) se = __builtin_inff();
+        else se = log2_exponent<T>(v, p.use_round);
+        se = T::round(se - p.ele_emax);
+        se = se < p.sc_emin ? p.sc_emin : (se > p.sc_emax ? p.sc_emax : se);
+        if (se != se) return se;
+        return T::round(pow2f((int)se));
+    }
+    return scale_quant<T>(T::round(amax / p.ele_maxnorm), p.sf);
+}
+
+template <class T, int M>
+__global__ __launch_bounds__(kThreads) void mxfp_qdq_kernel(const typename T::storage* __restrict__ x,
+                                                            typename T::storage* __restrict__ y,
+                                                            typename T::storage* __restrict__ scales,
+                                                            uint8_t* __restrict__ codes, int64_t cols, int block,
+                                                            int lpb_log2, int64_t nblk_row, int64_t nb, MxParams p, bool ragged) {
+    const Locate L = locate(lpb_log2, nblk_row, nb, block);
+    float v[kV];
+    load_lane<T>(x, L, cols, v, ragged);
+    if (p.per_tensor) {
+#pragma unroll
+        for (int i = 0; i < kV; ++i) v[i] = T::round(v[i] / p.tscale);
+    }
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < kV; ++i) {
+        uint32_t b = f2bits(v[i]) & 0x7fffffffu;
+        m = m > b ? m : b;
+    }
+    m = group_max_bits(m, 1 << lpb_log2);
+    const float s = mx_shared_scale<T>(bits2f(m), p);
+    const float rs = 1.0f / s;
+    uint32_t c[kV];
+#pragma unroll
+    for (int i = 0; i < kV; ++i) {
+        // a power-of-two scale divides exactly: rounding x * 2^-e is R_T(x / s)
+        float yv = p.pot ? T::round(v[i] * rs) : div_T<T>(v[i], s, rs);
+        float q = elem_quant<T, M>(yv, c[i]);
+        float o = T::round(q * s);
+        if (p.per_tensor) o = T::round(o * p.tscale);
+        v[i] = o;
+    }
+    store_lane<T>(y, L, cols, v, ragged);
+    if (L.valid) {
+        store_codes<M>(codes, L.row, cols, L.c0, c, ragged);
+        if (scales != nullptr && L.li == 0) scales[L.gb] = T::store(s);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// HBQ  (HBQQuantizer.quant_scale + q, src/quantizer.py:735-859)
+// ---------------------------------------------------------------------------
+constexpr int kMaxJ = 8;
+
+struct HbqParams {
+    int J;                       // number of L2 candidates (2^l2_sc_bit)
+    float l2[kMaxJ][2];          // L2 factors per candidate and scheme, in T
+    float rl2[kMaxJ][2];         // correctly rounded reciprocals
+    float em[2];                 // R_T(ele_max * max_j l2[j, s])
+    ScaleFmt sf;                 // E5M3 L1 scale format
+};
+
+__device__ __forceinline__ bool better(float v, float best) { return (v != v) ? (best == best) : (v < best); }
+
+// torch's fp32 order for the block error of one scheme (four interleaved
+// cascades over the 128.. elements, combined left to right), computed by the
+// lanes of one block.  sq holds this lane's 16 squared errors.
+__device__ __forceinline__ float block_row_sum(const float* sq, int li, int lpb, int lane_base) {
+    const int cl = lpb < 4 ? lpb : 4;                 // lanes per 16-term chunk
+    float run[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int step = 0; step < cl; ++step) {
+        float prev[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) prev[k] = __shfl_up(run[k], 1, 64);
+        if ((li % cl) == step) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                float a = step == 0 ? 0.f : prev[k];
+                a += sq[k];
+                a += sq[k + 4];
+                a += sq[k + 8];
+                a += sq[k + 12];
+                run[k] = a;
+            }
+        }
+    }
+    const int nchunks = lpb / cl;
+    float P[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) P[k] = __shfl(run[k], lane_base + cl - 1, 64);
+    for (int c = 1; c < nchunks; ++c) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) P[k] += __shfl(run[k], lane_base + c * cl + cl - 1, 64);
+    }
+    return ((P[0] + P[1]) + P[2]) + P[3];
+}
+
+template <class T, int M, int L2B, int S>
+__global__ __launch_bounds__(kThreads) void hbq_qdq_kernel(const typename T::storage* __restrict__ x,
+                                                           typename T::storage* __restrict__ y,
+                                                           typename T::storage* __restrict__ l1_out,
+                                                           uint8_t* __restrict__ l2i_out, uint8_t* __restrict__ sch_out,
+                                                           uint8_t* __restrict__ codes, int64_t cols, int block,
+                                                           int lpb_log2, int64_t nblk_row, int64_t nb, HbqParams p, bool ragged) {
+    constexpr int NSUBL = L2B <= kV ? kV / L2B : 1;   // sub-blocks held by one lane
+    constexpr int LPS = L2B <= kV ? 1 : L2B / kV;     // lanes per sub-block
+    const Locate L = locate(lpb_log2, nblk_row, nb, block);
+    const int lpb = 1 << lpb_log2;
+    const int lane = (int)(threadIdx.x & 63);
+    const int lane_base = lane - L.li;
+
+    float xv[kV];
+    load_lane<T>(x, L, cols, xv, ragged);
+
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < kV; ++i) {
+        uint32_t b = f2bits(xv[i]) & 0x7fffffffu;
+        m = m > b ? m : b;
+    }
+    const float amax = bits2f(group_max_bits(m, lpb));
+
+    float l1[S];
+    float dsel[S][kV], sqsel[S][kV];
+    uint32_t csel[S][kV];
+    int jsel[S][NSUBL];
+
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        l1[s] = scale_quant<T>(T::round(amax / p.em[s]), p.sf);
+        const float rl1 = 1.0f / l1[s];
+        float t[kV];
+#pragma unroll
+        for (int i = 0; i < kV; ++i) t[i] = div_T<T>(xv[i], l1[s], rl1);
+        float best[NSUBL];
+        for (int j = 0; j < p.J; ++j) {
+            const float l2 = p.l2[j][s], rl2 = p.rl2[j][s];
+            float dj[kV], sqj[kV];
+            uint32_t cj[kV];
+#pragma unroll
+            for (int i = 0; i < kV; ++i) {
+                float u = (l2 == 1.0f) ? t[i] : div_T<T>(t[i], l2, rl2);
+                float q = elem_quant<T, M>(u, cj[i]);
+                float d = T::round(T::round(q * l2) * l1[s]);
+                float e = T::round(xv[i] - d);
+                dj[i] = d;
+                sqj[i] = T::round(e * e);
+            }
+#pragma unroll
+            for (int sb = 0; sb < NSUBL; ++sb) {
+                constexpr int n = L2B <= kV ? L2B : kV;
+                float acc = 0.f;
+#pragma unroll
+                for (int i = 0; i < n; ++i) acc += sqj[sb * n + i];
+                if (LPS > 1) {
+                    // sub-block spans LPS lanes: fold their 16-term sums in lane order
+                    const int first = lane - (L.li % LPS);
+                    float tot = __shfl(acc, first, 64);
+                    for (int k = 1; k < LPS; ++k) tot += __shfl(acc, first + k, 64);
+                    acc = tot;
+                }
+                const float sse = T::round(acc);
+                if (j == 0 || better(sse, best[sb])) {
+                    best[sb] = sse;
+                    jsel[s][sb] = j;
+#pragma unroll
+                    for (int i = 0; i < n; ++i) {
+                        dsel[s][sb * n + i] = dj[sb * n + i];
+                        sqsel[s][sb * n + i] = sqj[sb * n + i];
+                        csel[s][sb * n + i] = cj[sb * n + i];
+                    }
+                }
+            }
+        }
+    }
+
+    int sstar = 0;
+    if constexpr (S == 2) {
+        float e0 = T::round(block_row_sum(sqsel[0], L.li, lpb, lane_base));
+        float e1 = T::round(block_row_sum(sqsel[S - 1], L.li, lpb, lane_base));
+        sstar = better(e1, e0) ? 1 : 0;
+    }
+
+    float out[kV];
+    uint32_t cout[kV];
+#pragma unroll
+    for (int i = 0; i < kV; ++i) {
+        out[i] = (S == 2 && sstar) ? dsel[S - 1][i] : dsel[0][i];
+        cout[i] = (S == 2 && sstar) ? csel[S - 1][i] : csel[0][i];
+    }
+    store_lane<T>(y, L, cols, out, ragged);
+    if (!L.valid) return;
+    store_codes<M>(codes, L.row, cols, L.c0, cout, ragged);
+    if (L.li == 0) {
+        if (l1_out) l1_out[L.gb] = T::store((S == 2 && sstar) ? l1[S - 1] : l1[0]);
+        if (sch_out) sch_out[L.gb] = (uint8_t)sstar;
+    }
+    if (l2i_out) {
+        const int nsub_blk = block / L2B;
+        if (L2B <= kV) {
+#pragma unroll
+            for (int sb = 0; sb < NSUBL; ++sb) {
+                l2i_out[L.gb * nsub_blk + (L.li * kV) / L2B + sb] =
+                        (uint8_t)((S == 2 && sstar) ? jsel[S - 1][sb] : jsel[0][sb]);
+            }
+        } else if ((L.li % LPS) == 0) {
+            l2i_out[L.gb * nsub_blk + (L.li * kV) / L2B] = (uint8_t)((S == 2 && sstar) ? jsel[S - 1][0] : jsel[0][0]);
+        }
+    }
+}
+
+// Elementwise fp_quant (src/quantizer.py:259-328), optionally after the clip
+// to the format's range that quant_scale applies (src/quantizer.py:735-739).
+template <class T>
+__global__ __launch_bounds__(kThreads) void scale_quant_kernel(const typename T::storage* __restrict__ x,
+                                                               typename T::storage* __restrict__ y, int64_t n,
+                                                               ScaleFmt f) {
+    int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    y[i] = T::store(scale_quant<T>(T::load(x[i]), f));
+}
+
+// Elementwise make_fp_quant (src/quantizer.py:187-257) for exhaustive checks of the element quantizer.
+template <class T, int M>
+__global__ __launch_bounds__(kThreads) void elem_quant_kernel(const typename T::storage* __restrict__ x,
+                                                              typename T::storage* __restrict__ y,
+                                                              uint8_t* __restrict__ codes, int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    uint32_t c;
+    float q = elem_quant<T, M>(T::load(x[i]), c);
+    y[i] = T::store(q);
+    if (codes) codes[i] = (uint8_t)c;
+}
+
+}  // namespace hbq
+
+// ===========================================================================
+// Host launchers
+// ===========================================================================
+using namespace hbq;
+
+namespace {
+
+int ilog2_exact(int v) {
+    int l = 0;
+    while ((1 << l) < v) ++l;
+    return (1 << l) == v ? l : -1;
+}
+
+double max_norm_h(int ebit, int mbit) {
+    if (ebit == 4 && mbit == 3) return 448.0;
+    int emax = (ebit == 5) ? 15 : (1 << (ebit - 1));
+    return ldexp(1.0, emax) * (double)((1 << (mbit + 1)) - 1) / (double)(1 << mbit);
+}
+double min_norm_h(int ebit) { return ebit == 1 ? 1.0 : ldexp(1.0, 2 - (1 << (ebit - 1))); }
+double min_subnorm_h(int ebit, int mbit) { return ldexp(1.0, 2 - (1 << (ebit - 1))) * ldexp(1.0, -mbit); }
+
+float round_host(double v, int dt) {
+    float f = (float)v;
+    if (dt == kF16) return (float)(_Float16)f;
+    if (dt == kBF16) {
+        uint32_t x;
+        memcpy(&x, &f, 4);
+        x += 0x7fffu + ((x >> 16) & 1u);
+        x &= 0xffff0000u;
+        memcpy(&f, &x, 4);
+    }
+    return f;
+}
+
+int scale_fmt(ScaleFmt& f, int sc_ebit, int sc_mbit, int allow_sub, int use_ceil) {
+    if (sc_ebit < 2 || sc_ebit > 5 || sc_mbit < 0 || sc_mbit > 7)
+        return hbq_fail(HBQ_ERR_UNSUPPORTED, "scale format E%dM%d is not supported on the GPU path", sc_ebit, sc_mbit);
+    int emin = 2 - (1 << (sc_ebit - 1));
+    int emax = sc_ebit == 5 ? 15 : (1 << (sc_ebit - 1));
+    f.lo = (float)(allow_sub ? min_subnorm_h(sc_ebit, sc_mbit) : min_norm_h(sc_ebit));
+    f.hi = (float)max_norm_h(sc_ebit, sc_mbit);
+    f.emin = (float)emin;
+    f.emax = (float)emax;
+    f.minn = (float)min_norm_h(sc_ebit);
+    f.thr = (float)(min_norm_h(sc_ebit) - ldexp(1.0, -(sc_mbit + 1)) * ldexp(1.0, emin));
+    f.mmax = (float)((1 << sc_mbit) - 1);
+    f.mshift = (float)(1 << sc_mbit);
+    f.allow_sub = allow_sub;
+    f.use_ceil = use_ceil;
+    f.e4m3 = (sc_ebit == 4 && sc_mbit == 3);
+    return 0;
+}
+
+struct Geometry {
+    int64_t nblk_row, nb;
+    int lpb_log2;
+    bool ragged;
+    unsigned grid;
+};
+
+int geometry(Geometry& g, const void* x, const void* y, const void* codes, int64_t rows, int64_t cols, int block,
+             int esize) {
+    if (rows < 0 || cols < 0) return hbq_fail(HBQ_ERR_INVALID, "negative shape");
+    int lb = ilog2_exact(block);
+    if (lb < 4 || lb > 10)
+        return hbq_fail(HBQ_ERR_UNSUPPORTED, "block_size %d is not supported on the GPU path (powers of two 16..1024)",
+                        block);
+    g.lpb_log2 = lb - 4;
+    g.nblk_row = (cols + block - 1) / block;
+    g.nb = rows * g.nblk_row;
+    g.ragged = (cols % block) != 0 || ((uintptr_t)x % 16) != 0 || ((uintptr_t)y % 16) != 0 ||
+               (codes != nullptr && ((uintptr_t)codes % 16) != 0) || ((cols * esize) % 16) != 0;
+    int64_t lanes = g.nb << g.lpb_log2;
+    int64_t grid = (lanes + kThreads - 1) / kThreads;
+    if (grid > 0x7fffffff) return hbq_fail(HBQ_ERR_INVALID, "tensor too large");
+    g.grid = (unsigned)grid;
+    return 0;
+}
+
+template <class T, int M>
+void launch_mx(const Geometry& g, const void* x, void* y, void* scales, void* codes, int64_t cols, int block,
+               const MxParams& p, hipStream_t st) {
+    using S = typename T::storage;
+    hipLaunchKernelGGL((mxfp_qdq_kernel<T, M>), dim3(g.grid), dim3(kThreads), 0, st, (const S*)x, (S*)y, (S*)scales,
+                       (uint8_t*)codes, cols, block, g.lpb_log2, g.nblk_row, g.nb, p, g.ragged);
+}
+
+template <class T>
+int dispatch_mx_m(int mbit, const Geometry& g, const void* x, void* y, void* scales, void* codes, int64_t cols,
+                  int block, const MxParams& p, hipStream_t st) {
+    switch (mbit) {
+        case 1: launch_mx<T, 1>(g, x, y, scales, codes, cols, block, p, st); return 0;
+        case 2: launch_mx<T, 2>(g, x, y, scales, codes, cols, block, p, st); return 0;
+        case 3: launch_mx<T, 3>(g, x, y, scales, codes, cols, block, p, st); return 0;
+        case 5: launch_mx<T, 5>(g, x, y, scales, codes, cols, block, p, st); return 0;
+        default: return hbq_fail(HBQ_ERR_UNSUPPORTED, "element format E2M%d is not supported on the GPU path", mbit);
+    }
+}
+
+template <class T, int M, int L2B, int S>
+void launch_hbq(const Geometry& g, const void* x, void* y, void* l1, void* l2i, void* sch, void* codes, int64_t cols,
+                int block, const HbqParams& p, hipStream_t st) {
+    using St = typename T::storage;
+    hipLaunchKernelGGL((hbq_qdq_kernel<T, M, L2B, S>), dim3(g.grid), dim3(kThreads), 0, st, (const St*)x, (St*)y,
+                       (St*)l1, (uint8_t*)l2i, (uint8_t*)sch, (uint8_t*)codes, cols, block, g.lpb_log2, g.nblk_row,
+                       g.nb, p, g.ragged);
+}
+
+template <class T, int M, int S>
+int dispatch_hbq_l2b(int l2b, const Geometry& g, const void* x, void* y, void* l1, void* l2i, void* sch, void* codes,
+                     int64_t cols, int block, const HbqParams& p, hipStream_t st) {
+    switch (l2b) {
+        case 4: launch_hbq<T, M, 4, S>(g, x, y, l1, l2i, sch, codes, cols, block, p, st); return 0;
+        case 8: launch_hbq<T, M, 8, S>(g, x, y, l1, l2i, sch, codes, cols, block, p, st); return 0;
+        case 16: launch_hbq<T, M, 16, S>(g, x, y, l1, l2i, sch, codes, cols, block, p, st); return 0;
+        case 32: launch_hbq<T, M, 32, S>(g, x, y, l1, l2i, sch, codes, cols, block, p, st); return 0;
+        default:
+            return hbq_fail(HBQ_ERR_UNSUPPORTED, "l2_block_size %d is not supported on the GPU path (4, 8, 16 or 32)",
+                            l2b);
+    }
+}
+
+template <class T>
+int dispatch_hbq(int mbit, int S, int l2b, const Geometry& g, const void* x, void* y, void* l1, void* l2i, void* sch,
+                 void* codes, int64_t cols, int block, const HbqParams& p, hipStream_t st) {
+#define HBQ_CASE(MB, SS)                                                                             \
+    if (mbit == MB && S == SS) return dispatch_hbq_l2b<T, MB, SS>(l2b, g, x, y, l1, l2i, sch, codes, cols, block, p, st);
+    HBQ_CASE(1, 1) HBQ_CASE(1, 2) HBQ_CASE(2, 1) HBQ_CASE(2, 2) HBQ_CASE(3, 1) HBQ_CASE(3, 2)
+#undef HBQ_CASE
+    return hbq_fail(HBQ_ERR_UNSUPPORTED, "element format E2M%d is not supported by the HBQ GPU path", mbit);
+}
+
+}  // namespace
+
+extern "C" {
+
+int hbq_mxfp_qdq(const void* x, void* y, void* scales, void* codes, int64_t rows, int64_t cols, int dtype,
+                 int block_size, int ebit, int mbit, int sc_ebit, int sc_mbit, int scale_allow_subnormal,
+                 int use_round, int use_ceil, int per_tensor_scale, double tensor_scale, void* stream) {
+    hbq_clear_error();
+    if (dtype != kF16 && dtype != kBF16 && dtype != kF32) return hbq_fail(HBQ_ERR_INVALID, "bad dtype code %d", dtype);
+    if (ebit != 2) return hbq_fail(HBQ_ERR_UNSUPPORTED, "element exponent bits %d not supported on the GPU path", ebit);
+    if (x == nullptr || y == nullptr) return hbq_fail(HBQ_ERR_INVALID, "null input/output pointer");
+    int esize = dtype == kF32 ? 4 : 2;
+    Geometry g;
+    if (int rc = geometry(g, x, y, codes, rows, cols, block_size, esize)) return rc;
+    if (g.nb == 0) return 0;
+    MxParams p{};
+    p.pot = sc_mbit == 0;
+    p.use_round = use_round;
+    p.ele_emax = (float)(1 << (ebit - 1));
+    if (p.pot) {
+        if (sc_ebit < 2 || sc_ebit > 8) return hbq_fail(HBQ_ERR_UNSUPPORTED, "PoT scale exponent bits %d", sc_ebit);
+        p.sc_emax = (float)((1 << (sc_ebit - 1)) - 1);
+        p.sc_emin = (float)(2 - (1 << (sc_ebit - 1)));
+        p.min_normal = dtype == kF32 ? 1.17549435e-38f : 6.103515625e-05f;
+    } else {
+        if (int rc = scale_fmt(p.sf, sc_ebit, sc_mbit, scale_allow_subnormal, use_ceil)) return rc;
+        p.ele_maxnorm = round_host(max_norm_h(ebit, mbit), dtype);
+    }
+    p.per_tensor = per_tensor_scale;
+    p.tscale = round_host(tensor_scale, dtype);
+    hipStream_t st = (hipStream_t)stream;
+    int rc;
+    if (dtype == kF16) rc = dispatch_mx_m<F16>(mbit, g, x, y, scales, codes, cols, block_size, p, st);
+    else if (dtype == kBF16) rc = dispatch_mx_m<BF16>(mbit, g, x, y, scales, codes, cols, block_size, p, st);
+    else rc = dispatch_mx_m<F32>(mbit, g, x, y, scales, codes, cols, block_size, p, st);
+    if (rc) return rc;
+    return hbq_check_launch("hbq_mxfp_qdq");
+}
+
+int hbq_hbq_qdq(const void* x, void* y, void* l1_scale, void* l2_index, void* scheme, void* codes, int64_t rows,
+                int64_t cols, int dtype, int block_size, int ebit, int mbit, int sc_ebit, int sc_mbit,
+                int l2_block_size, int l2_sc_bit, int l2_scheme, int scale_allow_subnormal, int use_ceil,
+                void* stream) {
+    hbq_clear_error();
+    if (dtype != kF16 && dtype != kBF16 && dtype != kF32) return hbq_fail(HBQ_ERR_INVALID, "bad dtype code %d", dtype);
+    if (ebit != 2) return hbq_fail(HBQ_ERR_UNSUPPORTED, "element exponent bits %d not supported on the GPU path", ebit);
+    if (x == nullptr || y == nullptr) return hbq_fail(HBQ_ERR_INVALID, "null input/output pointer");
+    if (l2_block_size <= 0 || block_size % l2_block_size != 0)
+        return hbq_fail(HBQ_ERR_INVALID, "block_size must be divisible by l2_block_size");
+    if (l2_sc_bit < 0 || l2_sc_bit > 3)
+        return hbq_fail(HBQ_ERR_UNSUPPORTED, "l2_sc_bit %d not supported on the GPU path (0..3)", l2_sc_bit);
+    int esize = dtype == kF32 ? 4 : 2;
+    Geometry g;
+    if (int rc = geometry(g, x, y, codes, rows, cols, block_size, esize)) return rc;
+    if (l2_block_size > block_size) return hbq_fail(HBQ_ERR_INVALID, "l2_block_size larger than block_size");
+    HbqParams p{};
+    p.J = 1 << l2_sc_bit;
+    // L2 candidate tables (src/quantizer.py:745-770), each entry rounded to T
+    const int J = p.J;
+    int S = 1;
+    for (int r = 0; r < J; ++r) {
+        double rr = r, b1 = 1 << l2_sc_bit, b2 = 1 << (l2_sc_bit + 1), b3 = 1 << (l2_sc_bit + 2);
+        double fp = 1 + rr / b1, fp10 = 1 + rr / b2;
+        double v;
+        switch (l2_scheme) {
+            case 0: v = ldexp(1.0, r); break;
+            case 1: v = rr + 1; break;
+            case 2: v = 1 + rr / 2; break;
+            case 3: v = fp; break;
+            case 4: v = 1 + (rr + 1) / b1; break;
+            case 5: v = fp10; break;
+            case 6: v = 1 + rr / b3; break;
+            case 7: v = fp; S = 2; break;
+            default: return hbq_fail(HBQ_ERR_INVALID, "Invalid L2 scheme code %d", l2_scheme);
+        }
+        p.l2[r][0] = round_host(v, dtype);
+        p.l2[r][1] = round_host(l2_scheme == 7 ? fp10 : v, dtype);
+        p.rl2[r][0] = 1.0f / p.l2[r][0];
+        p.rl2[r][1] = 1.0f / p.l2[r][1];
+    }
+    float elemax = round_host(max_norm_h(ebit, mbit), dtype);
+    for (int s = 0; s < S; ++s) {
+        float m = p.l2[0][s];
+        for (int j = 1; j < J; ++j) m = p.l2[j][s] > m ? p.l2[j][s] : m;
+        p.em[s] = round_host((double)elemax * (double)m, dtype);
+    }
+    if (int rc = scale_fmt(p.sf, sc_ebit, sc_mbit, scale_allow_subnormal, use_ceil)) return rc;
+    if (g.nb == 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    int rc;
+    if (dtype == kF16) rc = dispatch_hbq<F16>(mbit, S, l2_block_size, g, x, y, l1_scale, l2_index, scheme, codes, cols, block_size, p, st);
+    else if (dtype == kBF16) rc = dispatch_hbq<BF16>(mbit, S, l2_block_size, g, x, y, l1_scale, l2_index, scheme, codes, cols, block_size, p, st);
+    else rc = dispatch_hbq<F32>(mbit, S, l2_block_size, g, x, y, l1_scale, l2_index, scheme, codes, cols, block_size, p, st);
+    if (rc) return rc;
+    return hbq_check_launch("hbq_hbq_qdq");
+}
+
+int hbq_scale_quant(const void* x, void* y, int64_t n, int dtype, int ebit, int mbit, int allow_subnormal,
+                    int use_ceil, int clip, void* stream) {
+    hbq_clear_error();
+    if (n < 0 || x == nullptr || y == nullptr) return hbq_fail(HBQ_ERR_INVALID, "bad arguments");
+    ScaleFmt f;
+    if (int rc = scale_fmt(f, ebit, mbit, allow_subnormal, use_ceil)) return rc;
+    if (!clip) {
+        f.lo = -__builtin_inff();
+        f.hi = __builtin_inff();
+    }
+    if (n == 0) return 0;
+    int64_t grid = (n + kThreads - 1) / kThreads;
+    if (grid > 0x7fffffff) return hbq_fail(HBQ_ERR_INVALID, "tensor too large");
+    hipStream_t st = (hipStream_t)stream;
+    if (dtype == kF16)
+        hipLaunchKernelGGL(scale_quant_kernel<F16>, dim3((unsigned)grid), dim3(kThreads), 0, st, (const uint16_t*)x,
+                           (uint16_t*)y, n, f);
+    else if (dtype == kBF16)
+        hipLaunchKernelGGL(scale_quant_kernel<BF16>, dim3((unsigned)grid), dim3(kThreads), 0, st, (const uint16_t*)x,
+                           (uint16_t*)y, n, f);
+    else if (dtype == kF32)
+        hipLaunchKernelGGL(scale_quant_kernel<F32>, dim3((unsigned)grid), dim3(kThreads), 0, st, (const float*)x,
+                           (float*)y, n, f);
+    else return hbq_fail(HBQ_ERR_INVALID, "bad dtype code %d", dtype);
+    return hbq_check_launch("hbq_scale_quant");
+}
+
+int hbq_elem_quant(const void* x, void* y, void* codes, int64_t n, int dtype, int ebit, int mbit, void* stream) {
+    hbq_clear_error();
+    if (ebit != 2) return hbq_fail(HBQ_ERR_UNSUPPORTED, "element exponent bits %d not supported on the GPU path", ebit);
+    if (n < 0 || x == nullptr || y == nullptr) return hbq_fail(HBQ_ERR_INVALID, "bad arguments");
+    if (n == 0) return 0;
+    int64_t grid = (n + kThreads - 1) / kThreads;
+    if (grid > 0x7fffffff) return hbq_fail(HBQ_ERR_INVALID, "tensor too large");
+    hipStream_t st = (hipStream_t)stream;
+#define ELEM_CASE(TT, MB)                                                                                          \
+    hipLaunchKernelGGL((elem_quant_kernel<TT, MB>), dim3((unsigned)grid), dim3(kThreads), 0, st,                   \
+                       (const TT::storage*)x, (TT::storage*)y, (uint8_t*)codes, n)
+#define ELEM_M(TT)                                                                                                 \
+    switch (mbit) {                                                                                                \
+        case 1: ELEM_CASE(TT, 1); break;                                                                           \
+        case 2: ELEM_CASE(TT, 2); break;                                                                           \
+        case 3: ELEM_CASE(TT, 3); break;                                                                           \
+        case 5: ELEM_CASE(TT, 5); break;                                                                           \
+        default: return hbq_fail(HBQ_ERR_UNSUPPORTED, "element format E2M%d not supported", mbit);               \
+    }
+    if (dtype == kF16) { ELEM_M(F16) }
+    else if (dtype == kBF16) { ELEM_M(BF16) }
+    else if (dtype == kF32) { ELEM_M(F32) }
+    else return hbq_fail(HBQ_ERR_INVALID, "bad dtype code %d", dtype);
+#undef ELEM_M
+#undef ELEM_CASE
+    return hbq_check_launch("hbq_elem_quant");
+}
+
+}  // extern "C"

@@ -1,0 +1,107 @@
+/*
+ * hbq_amd.h -- C ABI of the MI355X (gfx950) HBQ hot path.
+ *
+ * Plain pointers and sizes only.  All tensor pointers are device pointers
+ * (HIP global memory), row-major and contiguous; `stream` is a hipStream_t
+ * (NULL = the legacy default stream).  Every entry point is asynchronous on
+ * `stream`, returns 0 on success and a nonzero HBQ_ERR_* code otherwise;
+ * hbq_last_error() then returns the message (thread local).
+ *
+ * dtype codes: 0 = fp16, 1 = bf16, 2 = fp32.  fp16/bf16 tensors are 16-bit
+ * patterns, fp32 tensors 32-bit floats.
+ *
+ * Blocks run along the last dimension: a tensor is passed as [rows, cols]
+ * with cols its last dimension; a ragged last block is zero padded, as
+ * _reshape_to_blocks does (src/quantizer.py:67-146).
+ *
+ * Element codes (optional output, NULL to skip): sign | 2-bit exponent field
+ * | m mantissa bits, exponent field 0 for subnormals, i.e. the OCP encodings
+ * of E2M1/E2M2/E2M3/E2M5.  E2M1 codes are packed two per byte (even column
+ * in the low nibble, row stride ceil(cols/2) bytes); wider codes take one byte
+ * per element (row stride cols).
+ */
+#ifndef HBQ_AMD_H
+#define HBQ_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HBQ_DTYPE_F16 0
+#define HBQ_DTYPE_BF16 1
+#define HBQ_DTYPE_F32 2
+
+#define HBQ_ERR_INVALID 1
+#define HBQ_ERR_UNSUPPORTED 2
+#define HBQ_ERR_HIP 3
+
+/* L2 scheme codes, in the order of HBQQuantizer.L2_SCHEME (src/quantizer.py:708) */
+#define HBQ_L2_POT 0
+#define HBQ_L2_INT 1
+#define HBQ_L2_SIG1 2
+#define HBQ_L2_FPM1 3
+#define HBQ_L2_FP1 4
+#define HBQ_L2_FPM10 5
+#define HBQ_L2_FPM100 6
+#define HBQ_L2_MIX 7
+
+/* Message of the last failing call on this thread ("" after a success). */
+const char *hbq_last_error(void);
+
+/* ABI revision of this header. */
+int hbq_abi_version(void);
+
+/*
+ * MXFP / NVFP quantize-dequantize.
+ * Replaces MXFPQuantizer.q (src/quantizer.py:513-539) together with
+ * MXFPQuantizer.get_shared_scale (src/quantizer.py:481-511): sc_mbit == 0
+ * selects the power-of-two scale (MXFP4/MXFP8), sc_mbit > 0 the FP scale
+ * (NVFP4 with E5M3).  y has x's shape and dtype; scales (optional) is
+ * [rows, ceil(cols/block_size)] in x's dtype; codes as described above.
+ * per_tensor_scale/tensor_scale carry MXFPQuantizer's per-tensor scale,
+ * computed by the caller from max|x| (src/quantizer.py:516-524).
+ * GPU limits: ebit == 2, mbit in {1,2,3,5}, block_size a power of two 16..1024.
+ */
+int hbq_mxfp_qdq(const void *x, void *y, void *scales, void *codes, int64_t rows, int64_t cols, int dtype,
+                 int block_size, int ebit, int mbit, int sc_ebit, int sc_mbit, int scale_allow_subnormal,
+                 int use_round, int use_ceil, int per_tensor_scale, double tensor_scale, void *stream);
+
+/*
+ * HBQ two-level quantize-dequantize.
+ * Replaces HBQQuantizer.q (src/quantizer.py:741-859) with its L1 scale
+ * HBQQuantizer.quant_scale (src/quantizer.py:735-739).  Outputs (each
+ * optional except y) mirror the keep_l2_scale attributes:
+ *   l1_scale [rows, nblk] in x's dtype          -> shared_scale
+ *   l2_index [rows, nblk, block/l2_block] uint8 -> l2_scale
+ *   scheme   [rows, nblk] uint8                 -> blk_l2_scheme
+ * GPU limits: ebit == 2, mbit in {1,2,3}, l2_block_size in {4,8,16,32},
+ * l2_sc_bit in 0..3, block_size a power of two 16..1024.
+ */
+int hbq_hbq_qdq(const void *x, void *y, void *l1_scale, void *l2_index, void *scheme, void *codes, int64_t rows,
+                int64_t cols, int dtype, int block_size, int ebit, int mbit, int sc_ebit, int sc_mbit,
+                int l2_block_size, int l2_sc_bit, int l2_scheme, int scale_allow_subnormal, int use_ceil,
+                void *stream);
+
+/*
+ * Elementwise E2Mm quantization with subnormals.
+ * Replaces the callable returned by make_fp_quant(ebit, mbit) (src/quantizer.py:187-257)
+ * and served by GLOBAL_FP_QUANT_CACHE (src/quantizer.py:38-65).  codes optional, one byte each.
+ */
+int hbq_elem_quant(const void *x, void *y, void *codes, int64_t n, int dtype, int ebit, int mbit, void *stream);
+
+/*
+ * Elementwise scale quantization to E(ebit)M(mbit), half-up (use_ceil=0) or
+ * ceil rounding.  clip=0 replaces fp_quant (src/quantizer.py:259-328);
+ * clip=1 first clips to the format's [min (sub)normal, max normal] range and
+ * replaces HBQQuantizer.quant_scale (src/quantizer.py:735-739).
+ */
+int hbq_scale_quant(const void *x, void *y, int64_t n, int dtype, int ebit, int mbit, int allow_subnormal,
+                    int use_ceil, int clip, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HBQ_AMD_H */

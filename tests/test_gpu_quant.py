@@ -1,0 +1,239 @@
+"""GPU parity of the fused quantizer kernels against the reference goldens and the CPU oracle.
+
+Every comparison is bit-exact (NaN positions compared as NaN)."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import TDT, mismatches, synth, to_bits, to_torch
+
+pytestmark = pytest.mark.gpu
+
+MXCFG = {
+    "mxfp4": dict(block_size=32, ebit=2, mbit=1, sc_ebit=5, sc_mbit=0),
+    "mxfp4_round": dict(block_size=32, ebit=2, mbit=1, sc_ebit=5, sc_mbit=0, use_round=True),
+    "mxfp8": dict(block_size=32, ebit=2, mbit=5, sc_ebit=5, sc_mbit=0),
+    "mxfp8_round": dict(block_size=32, ebit=2, mbit=5, sc_ebit=5, sc_mbit=0, use_round=True),
+    "nvfp4": dict(block_size=16, ebit=2, mbit=1, sc_ebit=5, sc_mbit=3),
+    "nvfp4_ceil": dict(block_size=16, ebit=2, mbit=1, sc_ebit=5, sc_mbit=3, use_ceil=True),
+}
+HBQCFG = {
+    "hbq_a_act": dict(ebit=2, mbit=2, l2_block_size=8, l2_sc_bit=2, l2_scheme="SIG-1"),
+    "hbq_a_wgt": dict(ebit=2, mbit=1, l2_block_size=8, l2_sc_bit=2, l2_scheme="Mix"),
+    "hbq_e_act": dict(ebit=2, mbit=2, l2_block_size=32, l2_sc_bit=2, l2_scheme="SIG-1"),
+    "hbq_e_wgt": dict(ebit=2, mbit=1, l2_block_size=32, l2_sc_bit=2, l2_scheme="Mix"),
+    "hbq_kv4": dict(ebit=2, mbit=1, l2_block_size=8, l2_sc_bit=2, l2_scheme="SIG-1"),
+    "hbq_a_wgt_ceil": dict(ebit=2, mbit=1, l2_block_size=8, l2_sc_bit=2, l2_scheme="Mix", use_ceil=True),
+    "hbq_pot": dict(ebit=2, mbit=1, l2_block_size=4, l2_sc_bit=1, l2_scheme="PoT"),
+}
+
+
+def _mx(kw, **extra):
+    from hbq_amd.quantizer import MXFPQuantizer
+    return MXFPQuantizer(scale_allow_subnormal=False, **kw, **extra)
+
+
+def _hbq(kw, **extra):
+    from hbq_amd.quantizer import HBQQuantizer
+    return HBQQuantizer(block_size=128, sc_ebit=5, sc_mbit=3, scale_allow_subnormal=False, **kw, **extra)
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("em", [(2, 1), (2, 2), (2, 5)])
+def test_element_quantizer_exhaustive(gpu, golden_elem, dt, em):
+    """make_fp_quant over all 65,536 bit patterns equals the reference table."""
+    from hbq_amd.quantizer import make_fp_quant
+    print(f"elem dt={dt} E{em[0]}M{em[1]}", flush=True)
+    allb = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    x = to_torch(allb, dt).to(gpu)
+    y = make_fp_quant(*em)(x)
+    assert mismatches(to_bits(y), golden_elem[f"elem_{dt}_e{em[0]}m{em[1]}"], dt) == 0
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("use_ceil", [False, True])
+@pytest.mark.parametrize("clip", [False, True])
+def test_scale_quantizer_vs_oracle(gpu, oracle, dt, use_ceil, clip):
+    """fp_quant / quant_scale to E5M3 against the oracle: every 16-bit pattern, or a wide fp32 sample."""
+    from hbq_amd.quantizer import HBQQuantizer, fp_quant
+    print(f"scale dt={dt} ceil={use_ceil} clip={clip}", flush=True)
+    if dt == "f32":
+        g = torch.Generator().manual_seed(5)
+        x = (torch.rand(1 << 20, generator=g) * 60 - 30).exp2() * torch.sign(torch.randn(1 << 20, generator=g))
+        xb = x.numpy()
+    else:
+        xb = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    xt = to_torch(xb, dt).to(gpu)
+    if clip:
+        y = HBQQuantizer(use_ceil=use_ceil).quant_scale(xt)
+        lo, hi = 2.0 ** -14, 61440.0
+        xc = to_torch(xb, dt).float().clamp(lo, hi).to(TDT[dt])
+        ref = oracle.fp_quant(to_bits(xc), dt, 5, 3, allow_subnormal=False, use_ceil=use_ceil)
+    else:
+        y = fp_quant(xt, 5, 3, allow_subnormal=False, use_ceil=use_ceil)
+        ref = oracle.fp_quant(xb, dt, 5, 3, allow_subnormal=False, use_ceil=use_ceil)
+    assert mismatches(to_bits(y), ref, dt) == 0
+
+
+@pytest.mark.parametrize("name", list(MXCFG))
+def test_mxfp_golden(gpu, golden_mxfp, name):
+    print(f"mxfp golden {name}", flush=True)
+    q = _mx(MXCFG[name])
+    x = to_torch(golden_mxfp["x_f16"], "f16").to(gpu)
+    assert mismatches(to_bits(q.q(x)), golden_mxfp[f"{name}_f16"], "f16") == 0
+    blocks = q.reshape(x)[0]
+    s = q.get_shared_scale(blocks).squeeze(-1)
+    assert mismatches(to_bits(s), golden_mxfp[f"{name}_f16_scale"], "f16") == 0
+    x32 = torch.from_numpy(golden_mxfp["x_f32"]).to(gpu)
+    assert mismatches(to_bits(q.q(x32)), golden_mxfp[f"{name}_f32"], "f32") == 0
+
+
+@pytest.mark.parametrize("name", ["mxfp4", "nvfp4"])
+def test_mxfp_golden_ragged(gpu, golden_mxfp, name):
+    print(f"mxfp ragged {name}", flush=True)
+    x = to_torch(golden_mxfp["x_ragged_f16"], "f16").to(gpu)
+    assert mismatches(to_bits(_mx(MXCFG[name]).q(x)), golden_mxfp[f"{name}_ragged_f16"], "f16") == 0
+
+
+def test_mxfp_bf16_raises(gpu):
+    """The reference's get_shared_scale rejects bf16 (src/quantizer.py:482-487)."""
+    with pytest.raises(NotImplementedError):
+        _mx(MXCFG["mxfp4"]).q(torch.zeros(4, 32, dtype=torch.bfloat16, device=gpu))
+
+
+@pytest.mark.parametrize("name", list(HBQCFG))
+@pytest.mark.parametrize("inp", ["f16", "f16w", "bf16"])
+def test_hbq_golden(gpu, golden_hbq, name, inp):
+    key = f"{name}_{inp}"
+    if key not in golden_hbq:
+        pytest.skip("no fixture")
+    print(f"hbq golden {key}", flush=True)
+    dt = "bf16" if inp == "bf16" else "f16"
+    q = _hbq(HBQCFG[name], keep_l2_scale=True)
+    x = to_torch(golden_hbq[f"x_{inp}"], dt).to(gpu)
+    y = q.q(x)
+    assert mismatches(to_bits(y), golden_hbq[key], dt) == 0
+    assert mismatches(to_bits(q.shared_scale), golden_hbq[key + "_l1"], dt) == 0
+    assert np.array_equal(q.l2_scale.cpu().numpy(), golden_hbq[key + "_l2idx"].astype(np.int64))
+    assert np.array_equal(q.blk_l2_scheme.cpu().numpy(), golden_hbq[key + "_scheme"].astype(np.int64))
+    assert mismatches(to_bits(q.real_l2_scale), golden_hbq[key + "_l2val"], dt) == 0
+
+
+def test_hbq_golden_ragged(gpu, golden_hbq):
+    x = to_torch(golden_hbq["x_ragged_f16"], "f16").to(gpu)
+    y = _hbq(HBQCFG["hbq_a_act"]).q(x)
+    assert mismatches(to_bits(y), golden_hbq["hbq_a_act_ragged_f16"], "f16") == 0
+
+
+def _edge_rows(x):
+    """Overwrite a few rows with zeros, +-inf, NaN, huge and subnormal values."""
+    x = x.clone()
+    x[0] = 0
+    x[1, ::7] = float("inf")
+    x[2, 5] = float("nan")
+    x[3, 3::11] = -float("inf")
+    x[4] = x[4] * 1e-6
+    x[5] = x[5].sign() * 60000
+    return x
+
+
+@pytest.mark.parametrize("name", list(HBQCFG))
+@pytest.mark.parametrize("dt", ["f16", "bf16", "f32"])
+def test_hbq_vs_oracle(gpu, oracle, name, dt):
+    """HBQ on a 256 x 4096 mixture with edge rows, all dtypes, against the oracle."""
+    print(f"hbq oracle {name} {dt}", flush=True)
+    x = _edge_rows(synth(256, 4096, 11, dt))
+    q = _hbq(HBQCFG[name], keep_l2_scale=True)
+    y = q.q(x.to(gpu))
+    ref = oracle.hbq_qdq(to_bits(x), dt, block_size=128, **HBQCFG[name])
+    assert mismatches(to_bits(y), ref["y"], dt) == 0
+    assert mismatches(to_bits(q.shared_scale), ref["l1"], dt) == 0
+    assert np.array_equal(q.l2_scale.cpu().numpy(), ref["l2idx"].astype(np.int64))
+    assert np.array_equal(q.blk_l2_scheme.cpu().numpy(), ref["scheme"].astype(np.int64))
+
+
+@pytest.mark.parametrize("name", list(MXCFG))
+@pytest.mark.parametrize("dt", ["f16", "f32"])
+def test_mxfp_vs_oracle(gpu, oracle, name, dt):
+    print(f"mxfp oracle {name} {dt}", flush=True)
+    x = _edge_rows(synth(256, 4096, 12, dt))
+    q = _mx(MXCFG[name])
+    out = q.quantize(x.to(gpu))
+    y, s = oracle.mxfp_qdq(to_bits(x), dt, **MXCFG[name])
+    assert mismatches(to_bits(out.y), y, dt) == 0
+    assert mismatches(to_bits(out.scales), s, dt) == 0
+
+
+@pytest.mark.parametrize("block,l2b", [(16, 4), (32, 8), (64, 16), (256, 32), (1024, 32)])
+@pytest.mark.parametrize("scheme", ["Mix", "SIG-1", "INT"])
+def test_hbq_block_shapes_vs_oracle(gpu, oracle, block, l2b, scheme):
+    """Other block / L2 block sizes and schemes, with a ragged last dimension."""
+    print(f"hbq shapes B={block} l2b={l2b} {scheme}", flush=True)
+    x = synth(64, 3 * block + 48, 13, "f16")
+    kw = dict(ebit=2, mbit=1, l2_block_size=l2b, l2_sc_bit=2, l2_scheme=scheme)
+    from hbq_amd.quantizer import HBQQuantizer
+    y = HBQQuantizer(block_size=block, sc_ebit=5, sc_mbit=3, **kw).q(x.to(gpu))
+    ref = oracle.hbq_qdq(to_bits(x), "f16", block_size=block, **kw)
+    assert mismatches(to_bits(y), ref["y"], "f16") == 0
+
+
+def test_hbq_config1_full(gpu, oracle):
+    """Config 1 tensor: bf16 4096 x 4096 ~ N(0,1) with a 0.5% Laplace(20) tail, HBQ-A/E act and wgt."""
+    x = synth(4096, 4096, 1001, "bf16", outliers=0)
+    xg = x.to(gpu)
+    for name in ("hbq_a_act", "hbq_a_wgt", "hbq_e_act", "hbq_e_wgt"):
+        print(f"config1 {name}", flush=True)
+        y = _hbq(HBQCFG[name]).q(xg)
+        ref = oracle.hbq_qdq(to_bits(x), "bf16", block_size=128, **HBQCFG[name])
+        assert mismatches(to_bits(y), ref["y"], "bf16") == 0, name
+
+
+def _decode(codes, mbit, n):
+    """Element values of E2Mm codes (sign | exp field | mantissa)."""
+    c = codes.astype(np.int64)
+    if mbit == 1:
+        c = np.stack([c & 0xF, c >> 4], axis=-1).reshape(c.shape[:-1] + (-1,))[..., :n]
+    sign = np.where((c >> (mbit + 2)) & 1, -1.0, 1.0)
+    ef = (c >> mbit) & 3
+    mf = c & ((1 << mbit) - 1)
+    mag = np.where(ef == 0, mf / 2.0 ** mbit, (1 + mf / 2.0 ** mbit) * 2.0 ** (ef - 1))
+    return sign * mag
+
+
+@pytest.mark.parametrize("name", ["hbq_a_act", "hbq_a_wgt", "hbq_e_wgt"])
+def test_hbq_codes_decode(gpu, name):
+    """Codes x L2 factor x L1 scale reproduce the dequantized output exactly."""
+    x = synth(128, 1024, 14, "f16")
+    q = _hbq(HBQCFG[name])
+    out = q.quantize(x.to(gpu))
+    mbit = HBQCFG[name]["mbit"]
+    vals = _decode(out.codes.cpu().numpy(), mbit, 1024)
+    tab = q.l2_table(dtype=torch.float32).numpy()
+    l2b = HBQCFG[name]["l2_block_size"]
+    l2 = tab[out.l2_index.cpu().numpy().astype(np.int64), out.scheme.cpu().numpy().astype(np.int64)[..., None]]
+    l2e = np.repeat(l2.reshape(128, -1), l2b, axis=1)
+    l1e = np.repeat(out.scales.float().cpu().numpy(), 128, axis=1)
+    dq = torch.from_numpy(vals * l2e).half().float().mul(torch.from_numpy(l1e)).half()
+    assert mismatches(to_bits(dq), to_bits(out.y), "f16") == 0
+
+
+@pytest.mark.parametrize("name", ["mxfp4", "mxfp8", "nvfp4"])
+def test_mxfp_codes_decode(gpu, name):
+    x = synth(128, 1024, 15, "f16")
+    q = _mx(MXCFG[name])
+    out = q.quantize(x.to(gpu))
+    B = MXCFG[name]["block_size"]
+    vals = _decode(out.codes.cpu().numpy(), MXCFG[name]["mbit"], 1024)
+    s = np.repeat(out.scales.float().cpu().numpy(), B, axis=1)
+    dq = torch.from_numpy(vals * s).half()
+    assert mismatches(to_bits(dq), to_bits(out.y), "f16") == 0
+
+
+def test_hbq_3d_input(gpu, oracle):
+    """Blocks run along the last dim of any-rank input; attributes keep the leading dims."""
+    x = synth(6 * 32, 256, 16, "f16").view(6, 32, 256)
+    q = _hbq(HBQCFG["hbq_kv4"], keep_l2_scale=True)
+    y = q.q(x.to(gpu))
+    assert y.shape == x.shape and q.shared_scale.shape == (6, 32, 2) and q.l2_scale.shape == (6, 32, 2, 16)
+    ref = oracle.hbq_qdq(to_bits(x.view(-1, 256)), "f16", block_size=128, **HBQCFG["hbq_kv4"])
+    assert mismatches(to_bits(y.view(-1, 256)), ref["y"], "f16") == 0
