@@ -1,0 +1,264 @@
+"""Throughput of the HBQ hot path on one MI355X.
+
+Workload: a bf16 [4096, 4096] tensor ~ N(0, 1) with
+0.5% of the entries replaced by Laplace(0, 20) samples, quantize-dequantized
+with HBQ-A activation settings (E2M2 elements, block 128, SIG-1 L2 over
+sub-blocks of 8, E5M3 L1 scale).  One step = one fused kernel launch that
+reads the tensor and writes the dequantized tensor, the element codes (one
+byte each) and the L1 / L2 / scheme scales.  `value` is the algorithmic HBM
+bytes of the step divided by the step time.
+
+The other formats of configs[1] and the block-quant GEMMs of configs[2..3] are
+measured in the same run and reported under "extra"; the CPU oracle is timed
+on the host cores as the baseline.
+
+Usage:  python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2516.6
+
+HBQ_CFGS = {
+    "hbq_a_act": dict(ebit=2, mbit=2, l2_block_size=8, l2_sc_bit=2, l2_scheme="SIG-1"),
+    "hbq_a_wgt": dict(ebit=2, mbit=1, l2_block_size=8, l2_sc_bit=2, l2_scheme="Mix"),
+    "hbq_e_act": dict(ebit=2, mbit=2, l2_block_size=32, l2_sc_bit=2, l2_scheme="SIG-1"),
+    "hbq_e_wgt": dict(ebit=2, mbit=1, l2_block_size=32, l2_sc_bit=2, l2_scheme="Mix"),
+}
+MX_CFGS = {
+    "mxfp4": dict(block_size=32, ebit=2, mbit=1, sc_ebit=5, sc_mbit=0),
+    "mxfp8": dict(block_size=32, ebit=2, mbit=5, sc_ebit=5, sc_mbit=0),
+    "nvfp4": dict(block_size=16, ebit=2, mbit=1, sc_ebit=5, sc_mbit=3),
+}
+
+
+def config1_tensor(dtype=torch.bfloat16, seed=1001):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(4096, 4096, generator=g)
+    n = x.numel()
+    idx = torch.randperm(n, generator=g)[: n // 200]
+    u = torch.rand(idx.numel(), generator=g) - 0.5
+    x.view(-1)[idx] = -20.0 * torch.sign(u) * torch.log1p(-2.0 * u.abs())
+    return x.to(dtype)
+
+
+def hbq_bytes_per_elem(cfg, elem_bytes=2, codes=True):
+    """Algorithmic HBM bytes per element: read + dequantized write + byte-aligned
+    codes + L1 (E5M3, one byte per block) + L2 index bits + scheme bit."""
+    b = 2.0 * elem_bytes
+    if codes:
+        b += 1.0
+        l2bits = 2 if cfg["l2_sc_bit"] == 2 else cfg["l2_sc_bit"]
+        b += 1.0 / 128 + l2bits / 8.0 / cfg["l2_block_size"]
+        if cfg["l2_scheme"] == "Mix":
+            b += 1.0 / 8 / 128
+    return b
+
+
+def mx_bytes_per_elem(cfg, elem_bytes=2, codes=True):
+    b = 2.0 * elem_bytes
+    if codes:
+        b += 0.5 if cfg["mbit"] == 1 else 1.0
+        b += 1.0 / cfg["block_size"]
+    return b
+
+
+class HipTimer:
+    """HIP events on torch's current stream (the stream the kernels run on)."""
+
+    def __init__(self):
+        self.a = torch.cuda.Event(enable_timing=True)
+        self.b = torch.cuda.Event(enable_timing=True)
+
+    def run(self, fn, iters):
+        self.a.record()
+        for _ in range(iters):
+            fn()
+        self.b.record()
+        self.b.synchronize()
+        return self.a.elapsed_time(self.b) / iters * 1e-3   # seconds per call
+
+
+def hbq_launcher(x, cfg, codes=True):
+    """Preallocated outputs + direct C-ABI launch (what a serving loop does)."""
+    from hbq_amd import _lib
+    from hbq_amd.quantizer import HBQQuantizer
+    L = _lib.lib()
+    rows, cols = x.shape
+    nblk = cols // 128
+    y = torch.empty_like(x)
+    c = torch.empty(rows, (cols + 1) // 2 if cfg["mbit"] == 1 else cols, dtype=torch.uint8, device=x.device) \
+        if codes else None
+    l1 = torch.empty(rows, nblk, dtype=x.dtype, device=x.device) if codes else None
+    l2 = torch.empty(rows, nblk, 128 // cfg["l2_block_size"], dtype=torch.uint8, device=x.device) if codes else None
+    sc = torch.empty(rows, nblk, dtype=torch.uint8, device=x.device) if codes else None
+    args = [_lib.ptr(x), _lib.ptr(y), _lib.ptr(l1), _lib.ptr(l2), _lib.ptr(sc), _lib.ptr(c), rows, cols,
+            _lib.DTYPE_CODE[x.dtype], 128, cfg["ebit"], cfg["mbit"], 5, 3, cfg["l2_block_size"], cfg["l2_sc_bit"],
+            HBQQuantizer.L2_SCHEME.index(cfg["l2_scheme"]), 0, 0, _lib.stream_of(x)]
+    fn = L.hbq_hbq_qdq
+
+    def step():
+        rc = fn(*args)
+        if rc:
+            _lib.check(rc)
+    return step, y
+
+
+def mx_launcher(x, cfg, codes=True):
+    from hbq_amd import _lib
+    L = _lib.lib()
+    rows, cols = x.shape
+    B = cfg["block_size"]
+    y = torch.empty_like(x)
+    c = torch.empty(rows, (cols + 1) // 2 if cfg["mbit"] == 1 else cols, dtype=torch.uint8, device=x.device) \
+        if codes else None
+    s = torch.empty(rows, cols // B, dtype=x.dtype, device=x.device) if codes else None
+    args = [_lib.ptr(x), _lib.ptr(y), _lib.ptr(s), _lib.ptr(c), rows, cols, _lib.DTYPE_CODE[x.dtype], B, cfg["ebit"],
+            cfg["mbit"], cfg["sc_ebit"], cfg["sc_mbit"], 0, 0, 0, 0, 1.0, _lib.stream_of(x)]
+    fn = L.hbq_mxfp_qdq
+
+    def step():
+        rc = fn(*args)
+        if rc:
+            _lib.check(rc)
+    return step, y
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def cpu_baseline(x_bits_cpu, cfg, bytes_per_elem, reps):
+    """The C oracle (port of the reference op sequence) on the host cores."""
+    from oracle import oracle as O
+    O.lib()
+    n = x_bits_cpu.size
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        O.hbq_qdq(x_bits_cpu, "bf16", block_size=128, **cfg)
+    dt = (time.perf_counter() - t0) / reps
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count())
+    return {"value": round(n * bytes_per_elem / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"full configs[1] tensor ({n} bf16 elements), HBQ-A act, {reps} repetitions, "
+                      f"{dt * 1e3:.0f} ms each; {cpu_model()}"}
+
+
+def load_traffic(name):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get(name)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--quick", action="store_true", help="headline only: skip the extra formats, GEMMs and CPU leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the HBQ hot path here has no multi-GPU mode (--gpus {args.gpus} "
+              f"requested). The quantizer and GEMM shard without communication; see DESIGN.md.", file=sys.stderr)
+        sys.exit(2)
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    x_cpu = config1_tensor()
+    x = x_cpu.to(dev)
+    cfg = HBQ_CFGS["hbq_a_act"]
+    step, _ = hbq_launcher(x, cfg)
+    bpe = hbq_bytes_per_elem(cfg)
+    n = x.numel()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timer = HipTimer()
+    t0 = time.perf_counter()
+    kernel_s = timer.run(step, args.steps)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall / args.steps * 1e3
+    value = n * bpe / (wall / args.steps) / 1e9
+    achieved = n * bpe / kernel_s / 1e9
+
+    extra = {"hbq_a_act_kernel_us": round(kernel_s * 1e6, 2), "bytes_per_elem": round(bpe, 4)}
+    if not args.quick:
+        # fake-quant-only (y only, 4 B/elem) and the other formats of configs[1]
+        s2, _ = hbq_launcher(x, cfg, codes=False)
+        t = HipTimer().run(s2, 100)
+        extra["hbq_a_act_fakequant_GBs"] = round(n * 4.0 / t / 1e9, 1)
+        for name, c in HBQ_CFGS.items():
+            if name == "hbq_a_act":
+                continue
+            s3, _ = hbq_launcher(x, c)
+            for _ in range(5):
+                s3()
+            t = HipTimer().run(s3, 100)
+            extra[f"{name}_GBs"] = round(n * hbq_bytes_per_elem(c) / t / 1e9, 1)
+            extra[f"{name}_frac"] = round(n * hbq_bytes_per_elem(c) / t / 1e9 / HBM_PEAK_GBS, 4)
+        x16 = x.to(torch.float16)   # MXFP/NVFP reject bf16 in the reference; same values in fp16
+        for name, c in MX_CFGS.items():
+            s4, _ = mx_launcher(x16, c)
+            for _ in range(5):
+                s4()
+            t = HipTimer().run(s4, 100)
+            extra[f"{name}_fp16_GBs"] = round(n * mx_bytes_per_elem(c) / t / 1e9, 1)
+        # device-to-device copy bandwidth for reference
+        dst = torch.empty_like(x)
+        t = HipTimer().run(lambda: dst.copy_(x), 100)
+        extra["d2d_copy_GBs"] = round(2 * x.numel() * 2 / t / 1e9, 1)
+        try:
+            from hbq_amd import gemm_bench
+            extra.update(gemm_bench.run(dev))
+        except ImportError:
+            pass
+
+    out = {
+        "metric": "HBQ quant-dequant GB/s + quant-GEMM TFLOP/s (% roofline), Llama-3-8B shapes",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "configs[1]: HBQ-A act quantize-dequantize (codes + scales) of a bf16 4096x4096 "
+                               "N(0,1) tensor with a 0.5% Laplace(20) tail", "elements": n, "block": 128,
+                   "l2_block": 8, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic("hbq_a_act_config1")},
+        "extra": extra,
+    }
+    if not args.quick:
+        bits = x_cpu.contiguous().view(torch.int16).numpy().view("uint16")
+        out["cpu_baseline"] = cpu_baseline(bits, cfg, bpe, reps=2)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()
