@@ -1,0 +1,44 @@
+"""Drop-in for the reference's src/ops.py: FP16AccumMatMul on the HIP GEMMs.
+
+Same constructor, forward(x, w, bias) signature, group-size validation
+(ValueError) and dispatch as src/ops.py:16-62.  The weight is handed to the
+kernel in its nn.Linear layout W[N, K] instead of materializing w.t() on
+every call (src/ops.py:41); the arithmetic is the same.
+"""
+import torch
+import torch.nn as nn
+
+from . import blockquant_ext as ext
+
+
+class FP16AccumMatMul(nn.Module):
+    """Low-precision-accumulation matmul: psum-quantized (quant_block_size set),
+    grouped fp16 (group_size set) or pure fp16 accumulation."""
+
+    def __init__(self, group_size: int = None, quant_block_size: int = None):
+        super().__init__()
+        self.group_size = group_size
+        self.quant_block_size = quant_block_size
+
+    def forward(self, x, w, bias=None) -> torch.Tensor:
+        orig_shape = x.shape
+        x2d = x.reshape(-1, x.shape[-1])
+        if x2d.dtype != torch.float16:
+            x2d = x2d.half()
+        x2d = x2d.to(w.device, non_blocking=True)
+        w16 = w if w.dtype == torch.float16 else w.half()
+        if self.quant_block_size is not None:
+            if self.group_size not in [4, 8, 16, 32, 64, 128]:
+                raise ValueError(f"Invalid group size: {self.group_size}")
+            if self.quant_block_size not in [4, 8, 16, 32]:
+                raise ValueError(f"Invalid quant block size: {self.quant_block_size}")
+            out2d = ext.gemm_blockquant_mxint8_nk(x2d, w16, self.group_size, self.quant_block_size)
+        elif self.group_size is not None:
+            if self.group_size not in [4, 8, 16, 32, 64, 128]:
+                raise ValueError(f"Invalid group size: {self.group_size}")
+            out2d = ext.gemm_fp16_grouped_accum_nk(x2d, w16, self.group_size)
+        else:
+            out2d = ext.gemm_fp16_accum_nk(x2d, w16)
+        if bias is not None:
+            out2d = out2d + bias
+        return out2d.view(*orig_shape[:-1], -1)
