@@ -134,6 +134,42 @@ def mx_launcher(x, cfg, codes=True):
     return step, y
 
 
+GEMM_CASES = [
+    # (name, M, K, N, op, group_k, group_n, weight layout)
+    ("cfg2_gateup_mxint8_kn", 4096, 4096, 14336, "mxint8", 128, 32, "kn"),
+    ("cfg2_gateup_mxint8_nk", 4096, 4096, 14336, "mxint8", 128, 32, "nk"),
+    ("cfg2_gateup_grouped_kn", 4096, 4096, 14336, "grouped", 128, 0, "kn"),
+    ("cfg2_down_grouped_kn", 4096, 14336, 4096, "grouped", 128, 0, "kn"),
+    ("cfg3_mxint8_kn", 8192, 4096, 4096, "mxint8", 128, 32, "kn"),
+]
+
+
+def gemm_extra(dev, cases=GEMM_CASES, iters=10):
+    """TFLOP/s (2MNK / kernel time) of the block-quant GEMMs at the configs[2..3] shapes."""
+    from hbq_amd import blockquant_ext as ext
+    out = {}
+    g = torch.Generator(device=dev).manual_seed(3)
+    for name, M, K, N, op, gk, gn, lay in cases:
+        A = torch.randn(M, K, device=dev, generator=g).half()
+        B = (torch.randn(N, K, device=dev, generator=g) * 0.02).half()
+        if lay == "kn":
+            B = B.t().contiguous()
+        nk = lay == "nk"
+        if op == "mxint8":
+            fn = lambda: ext.gemm_blockquant_mxint8(A, B, gk, gn, b_is_nk=nk)
+        else:
+            fn = lambda: ext.gemm_fp16_grouped_accum(A, B, gk, b_is_nk=nk)
+        for _ in range(2):
+            fn()
+        t = HipTimer().run(fn, iters)
+        tf = 2.0 * M * N * K / t / 1e12
+        out[f"{name}_TFLOPs"] = round(tf, 1)
+        out[f"{name}_frac"] = round(tf / FP16_PEAK_TFLOPS, 4)
+        out[f"{name}_ms"] = round(t * 1e3, 3)
+        del A, B
+    return out
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -174,6 +210,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only: skip the extra formats, GEMMs and CPU leg")
+    ap.add_argument("--gemm-only", action="store_true", help="print only the GEMM measurements")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the HBQ hot path here has no multi-GPU mode (--gpus {args.gpus} "
@@ -182,6 +219,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.gemm_only:
+        print(json.dumps(gemm_extra(dev)))
+        return
 
     x_cpu = config1_tensor()
     x = x_cpu.to(dev)
@@ -228,11 +268,7 @@ def main():
         dst = torch.empty_like(x)
         t = HipTimer().run(lambda: dst.copy_(x), 100)
         extra["d2d_copy_GBs"] = round(2 * x.numel() * 2 / t / 1e9, 1)
-        try:
-            from hbq_amd import gemm_bench
-            extra.update(gemm_bench.run(dev))
-        except ImportError:
-            pass
+        extra.update(gemm_extra(dev))
 
     out = {
         "metric": "HBQ quant-dequant GB/s + quant-GEMM TFLOP/s (% roofline), Llama-3-8B shapes",

@@ -274,8 +274,8 @@ class MXFPQuantizer(_QBase):
         return 1.0 if x_max == 0 else x_max / (ele_max * sc_max)
 
     def _run(self, x, block_size, want_codes, want_scales):
-        _lib.require_gpu(x, type(self).__name__)
         self._check_dtype(x)
+        _lib.require_gpu(x, type(self).__name__)
         xc, rows, cols = _as_rows(x)
         y = torch.empty_like(xc)
         nblk = -(-cols // block_size) if cols else 0
@@ -353,8 +353,8 @@ class HBQQuantizer(MXFPQuantizer):
         return tabs[self.l2_scheme][..., None]
 
     def _run_hbq(self, x, want_codes, want_stats):
-        _lib.require_gpu(x, "HBQQuantizer")
         self._check_dtype(x)
+        _lib.require_gpu(x, "HBQQuantizer")
         xc, rows, cols = _as_rows(x)
         B = self.block_size
         nblk = -(-cols // B) if cols else 0

@@ -100,6 +100,43 @@ int hbq_elem_quant(const void *x, void *y, void *codes, int64_t n, int dtype, in
 int hbq_scale_quant(const void *x, void *y, int64_t n, int dtype, int ebit, int mbit, int allow_subnormal,
                     int use_ceil, int clip, void *stream);
 
+/*
+ * Block-quant GEMMs of blockquant_ext.  A is [M,K] fp16, C is [M,N] fp16 (caller
+ * allocated, fully written).  With b_is_nk == 0, B is [K,N] fp16 as the
+ * reference ops take it (blockquant_ext.cpp:12-19); with b_is_nk == 1 it is the
+ * weight W[N,K] (same arithmetic, no transpose copy needed by the caller).
+ * In-group sums use MFMA fp32 accumulation; the cross-group fp16 accumulation
+ * and the psum quantization follow the reference step by step.
+ */
+
+/* Replaces gemm_fp32_accum -> gemm_fp32_accum_cuda (blockquant_ext.cpp:21-29, gemm.cu:593-616). */
+int hbq_gemm_fp32_accum(const void *A, const void *B, void *C, int64_t M, int64_t N, int64_t K, int b_is_nk,
+                        void *stream);
+
+/* Replaces gemm_fp16_accum -> gemm_fp16_accum_cuda (blockquant_ext.cpp:31-39, gemm.cu:568-591):
+ * one fused fp16 multiply-add per k in ascending order (bit-exact for any input). */
+int hbq_gemm_fp16_accum(const void *A, const void *B, void *C, int64_t M, int64_t N, int64_t K, int b_is_nk,
+                        void *stream);
+
+/* Replaces gemm_fp16_grouped_accum (blockquant_ext.cpp:41-49, gemm.cu:618-667); group_k in {16,32,64,128}. */
+int hbq_gemm_fp16_grouped_accum(const void *A, const void *B, void *C, int64_t M, int64_t N, int64_t K,
+                                int group_k, int b_is_nk, void *stream);
+
+/* Replaces gemm_blockquant_mxint8 (blockquant_ext.cpp:64-71, gemm.cu:1399-1478);
+ * group_k in {64,128,256}, group_n in {4,8,16,32}, K % group_k == 0, N % group_n == 0. */
+int hbq_gemm_blockquant_mxint8(const void *A, const void *B, void *C, int64_t M, int64_t N, int64_t K,
+                               int group_k, int group_n, int b_is_nk, void *stream);
+
+/* Replaces gemm_blockquant_mxfp8 (blockquant_ext.cpp:55-62, gemm.cu:1040-1135); same limits as mxint8. */
+int hbq_gemm_blockquant_mxfp8(const void *A, const void *B, void *C, int64_t M, int64_t N, int64_t K,
+                              int group_k, int group_n, int b_is_nk, void *stream);
+
+/* No reference counterpart: writes the fp32 partial sum of every group_k-wide K
+ * group, P[ceil(K/group_k), M, N], from the same MFMA accumulation as the GEMMs,
+ * so a test can apply the reference epilogue to exactly the kernel's partials. */
+int hbq_gemm_group_partials(const void *A, const void *B, void *P, int64_t M, int64_t N, int64_t K, int group_k,
+                            int b_is_nk, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

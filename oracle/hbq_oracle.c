@@ -247,6 +247,9 @@ static float cascade_sum(const float *v, int64_t n, int64_t stride) {
     return acc[0];
 }
 
+/* exported for the tests that pin the order against torch.sum */
+float orc_cascade_sum(const float *v, int64_t n, int64_t stride) { return cascade_sum(v, n, stride); }
+
 /* four interleaved cascades combined left to right (torch's row_sum) */
 static float row_sum(const float *v, int64_t n) {
     int64_t nilp = n / 4;
@@ -257,6 +260,8 @@ static float row_sum(const float *v, int64_t n) {
     for (int k = 1; k < 4; ++k) s += part[k];
     return s;
 }
+
+float orc_row_sum(const float *v, int64_t n) { return row_sum(v, n); }
 
 /* ------------------------------------------------------------------------- */
 /* exported scalar tables                                                     */

@@ -49,6 +49,10 @@ def lib():
             "orc_group_partials": [P, P, P, I, I, I, I],
             "orc_epilogue": [P, P, I, I, I, I, I],
         }
+        L.orc_cascade_sum.argtypes = [P, I64, I64]
+        L.orc_cascade_sum.restype = ctypes.c_float
+        L.orc_row_sum.argtypes = [P, I64]
+        L.orc_row_sum.restype = ctypes.c_float
         for name, args in sig.items():
             fn = getattr(L, name)
             fn.argtypes = args
@@ -153,6 +157,18 @@ def hbq_qdq(x, dt, block_size=128, ebit=2, mbit=3, sc_ebit=5, sc_mbit=3, l2_bloc
                              mbit, sc_ebit, sc_mbit, l2_block_size, l2_sc_bit, SCHEMES.index(l2_scheme),
                              int(scale_allow_subnormal), int(use_ceil)), "hbq_qdq")
     return {"y": y, "l1": l1, "l2idx": l2i, "scheme": sch, "l2val": l2v}
+
+
+def cascade_sum(v):
+    """torch's fp32 order for a Half sum over one strided column (sub-block errors)."""
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    return float(lib().orc_cascade_sum(_p(v), v.size, 1))
+
+
+def row_sum(v):
+    """torch's fp32 order for a Half sum over a contiguous row read with a stride (scheme errors)."""
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    return float(lib().orc_row_sum(_p(v), v.size))
 
 
 def _gemm_in(A, B):

@@ -1,0 +1,66 @@
+"""The C-ABI library loads and exports every entry point include/hbq_amd.h declares (no GPU calls)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "hbq_amd.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(hbq_\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from hbq_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        from hbq_amd import build
+        build.build(verbose=False)
+    return ctypes.CDLL(_lib.LIB_PATH)
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    for s in ("hbq_mxfp_qdq", "hbq_hbq_qdq", "hbq_elem_quant", "hbq_scale_quant", "hbq_gemm_fp32_accum",
+              "hbq_gemm_fp16_accum", "hbq_gemm_fp16_grouped_accum", "hbq_gemm_blockquant_mxint8",
+              "hbq_gemm_blockquant_mxfp8", "hbq_gemm_group_partials", "hbq_last_error", "hbq_abi_version"):
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+
+
+def test_python_signatures_cover_header():
+    from hbq_amd import _lib
+    assert set(declared_symbols()) <= set(_lib.SIGNATURES)
+
+
+def test_abi_version_and_error_string(lib):
+    lib.hbq_abi_version.restype = ctypes.c_int
+    assert lib.hbq_abi_version() == 1
+    lib.hbq_last_error.restype = ctypes.c_char_p
+    assert lib.hbq_last_error() == b""
+
+
+def test_argument_errors_without_gpu(lib):
+    """Argument checks fail before any HIP call, with the reference's messages."""
+    from hbq_amd import _lib
+    L = _lib.lib()
+    rc = L.hbq_gemm_fp16_grouped_accum(None, None, None, 4, 4, 4, 48, 0, None)
+    assert rc == 1 and L.hbq_last_error() == b"group_k must be one of {16,32,64,128}"
+    rc = L.hbq_gemm_blockquant_mxint8(None, None, None, 4, 4, 4, 128, 7, 0, None)
+    assert rc == 1 and b"group_n must be one of {4,8,16,32}" in L.hbq_last_error()
+    fake = ctypes.c_void_p(256)            # never dereferenced: the shape check fails first
+    rc = L.hbq_gemm_blockquant_mxint8(fake, fake, fake, 4, 32, 100, 128, 32, 0, None)
+    assert rc == 1 and L.hbq_last_error() == b"K must be divisible by group_k"
+    rc = L.hbq_hbq_qdq(None, None, None, None, None, None, 1, 128, 0, 128, 2, 2, 5, 3, 8, 2, 9, 0, 0, None)
+    assert rc == 1
+    rc = L.hbq_mxfp_qdq(ctypes.c_void_p(16), ctypes.c_void_p(16), None, None, 1, 96, 0, 48, 2, 1, 5, 0, 0, 0, 0,
+                        0, 1.0, None)
+    assert rc == 2 and b"block_size" in L.hbq_last_error()

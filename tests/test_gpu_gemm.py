@@ -119,7 +119,7 @@ def test_general_inputs_tolerance(gpu, oracle, op):
     else:
         got, ref = ext.gemm_blockquant_mxint8(Ad, Bd, 128, 32), oracle.gemm_blockquant_mxint8(b16(A), b16(B), 128, 32)
     rel, frac = _rel_err(got, ref)
-    print(f"{op}: max rel err {rel:.2e}, differing elements {frac:.4%}", flush=True)
+    print(f"{op}: normwise rel err {rel:.2e}, differing elements {frac:.4%}", flush=True)
     assert rel <= 1e-3
 
 
@@ -136,7 +136,7 @@ def test_hbq_quantized_operands_match(gpu, oracle):
     got = _ext().gemm_blockquant_mxint8_nk(Xq, Wq, 128, 32)
     ref = oracle.gemm_blockquant_mxint8(b16(Xq), b16(Wq.t().contiguous()), 128, 32)
     rel, frac = _rel_err(got, ref)
-    print(f"HBQ-E operands: max rel err {rel:.2e}, differing elements {frac:.4%}", flush=True)
+    print(f"HBQ-E operands: normwise rel err {rel:.2e}, differing elements {frac:.4%}", flush=True)
     assert rel <= 1e-3
 
 
