@@ -19,6 +19,7 @@ _P, _I, _I64, _D = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_doubl
 SIGNATURES = {
     "hbq_last_error": ([], ctypes.c_char_p),
     "hbq_abi_version": ([], _I),
+    "hbq_set_generic_only": ([_I], _I),
     "hbq_mxfp_qdq": ([_P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _D, _P], _I),
     "hbq_hbq_qdq": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "hbq_elem_quant": ([_P, _P, _P, _I64, _I, _I, _I, _P], _I),

@@ -1,0 +1,439 @@
+// Table-driven HBQ quantize-dequantize (fp16 / bf16 inputs, the configurations
+// of the HBQ-A/E formats).
+//
+// After the L1 division t = R_T(|x| / l1) the rest of the candidate chain of
+// HBQQuantizer.q (src/quantizer.py:781-791) depends on t alone: for every L2
+// candidate j the element level of R_T(t / l2_j) is a fixed function of the
+// 16-bit value t.  So
+//   * a level table indexed by the bits of t (the binades where the level is
+//     not constant) holds the levels of all J <= 4 candidates in one 32-bit
+//     word; it is built once per device and configuration on the GPU with the
+//     same device element quantizer as the generic kernel, and copied to LDS
+//     by each (persistent) workgroup;
+//   * per block, the dequantized magnitudes R_T(R_T(level * l2_j) * l1) of
+//     every (scheme, candidate, level) are tabulated in LDS by the block's lanes.
+// Per element and candidate what remains is the exact error arithmetic of the
+// reference: e = R_T(|x| - d), sq = R_T(e^2), and the fp32 sub-block sums in
+// torch's order (src/quantizer.py:802).  Signs never change an error, so the
+// candidate search runs on magnitudes; the sign of the output follows the
+// reference's zero rules (src/quantizer.py:241-245).
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <mutex>
+#include <stdint.h>
+#include <string.h>
+
+#include "hbq_capi_internal.h"
+#include "hbq_fast.h"
+#include "quant_common.h"
+
+namespace hbq {
+
+constexpr int kLutSlots = 16;
+constexpr int kLutMaxBinades = 12;
+constexpr int kLutMaxEntries = 2 * (kLutMaxBinades * 1024 + 2);
+constexpr int kFastJ = 4;
+
+// level tables: per slot, S schemes of (n + 2) words: [0] below the table range
+// (all levels 0), [1 .. n] the binades [2^lo, 2^hi), [n + 1] at or above 2^hi (saturated)
+static __device__ uint32_t g_lut[kLutSlots][kLutMaxEntries];
+// per slot: z[s][j] = smallest t > 0 with R_T(t / l2[j][s]) != 0, then a status word
+static __device__ float g_lut_z[kLutSlots][2 * kFastJ];
+static __device__ int g_lut_status[kLutSlots];
+
+struct FastParams {
+    int S, J, L;               // schemes, candidates, levels (2^(m+2))
+    int n;                     // table words per scheme, sentinels excluded
+    uint32_t lo_bits;          // T bit pattern of 2^lo
+    float l2[kFastJ][2];       // L2 factors
+    float em[2];
+    ScaleFmt sf;
+};
+
+template <class T>
+__device__ __forceinline__ uint32_t bits_of(float v) {
+    return (uint32_t)T::store(v);
+}
+
+template <class T>
+__device__ __forceinline__ float from_bits(uint32_t b) {
+    return T::load((typename T::storage)b);
+}
+
+// magnitude code of the element quantizer = its level (exponent field and mantissa)
+template <class T, int M>
+__device__ __forceinline__ uint32_t level_of(float u) {
+    uint32_t c;
+    elem_quant<T, M>(u, c);
+    return c & ((1u << (M + 2)) - 1u);
+}
+
+template <class T, int M>
+__global__ void build_lut_kernel(int slot, FastParams p) {
+    const int per = p.n + 2;
+    const int total = p.S * per;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
+        const int s = i / per, k = i % per;
+        uint32_t w = 0;
+        if (k == per - 1) {
+            for (int j = 0; j < p.J; ++j) w |= ((1u << (M + 2)) - 1u) << (8 * j);
+        } else if (k > 0) {
+            const float t = from_bits<T>(p.lo_bits + (uint32_t)(k - 1));
+            for (int j = 0; j < p.J; ++j) w |= level_of<T, M>(T::round(t / p.l2[j][s])) << (8 * j);
+        }
+        g_lut[slot][i] = w;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        int status = 0;
+        // the constant ends of the table: the largest value below 2^lo has level 0,
+        // 2^hi is already saturated, for every candidate
+        const float below = from_bits<T>(p.lo_bits - 1u);
+        const float top = from_bits<T>(p.lo_bits + (uint32_t)p.n);
+        for (int s = 0; s < p.S; ++s)
+            for (int j = 0; j < p.J; ++j) {
+                if (level_of<T, M>(T::round(below / p.l2[j][s])) != 0) status = 1;
+                if (level_of<T, M>(T::round(top / p.l2[j][s])) != (1u << (M + 2)) - 1u) status = 2;
+                float z = -1.f;
+                for (uint32_t b = 1; b < 4096 && z < 0.f; ++b) {
+                    const float t = from_bits<T>(b);
+                    if (T::round(t / p.l2[j][s]) != 0.f) z = t;
+                }
+                if (z < 0.f) status = 3;
+                g_lut_z[slot][s * kFastJ + j] = z;
+            }
+        g_lut_status[slot] = status;
+    }
+}
+
+template <class T, int M, int L2B, int S>
+__global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::storage* __restrict__ x,
+                                                            typename T::storage* __restrict__ y,
+                                                            typename T::storage* __restrict__ l1_out,
+                                                            uint8_t* __restrict__ l2i_out,
+                                                            uint8_t* __restrict__ sch_out,
+                                                            uint8_t* __restrict__ codes, int64_t cols, int block,
+                                                            int lpb_log2, int64_t nb, int slot, FastParams p) {
+    constexpr int L = 1 << (M + 2);
+    constexpr int NSUBL = L2B <= kV ? kV / L2B : 1;
+    constexpr int LPS = L2B <= kV ? 1 : L2B / kV;
+    extern __shared__ uint32_t smem[];
+    const int per = p.n + 2;
+    uint32_t* lut = smem;
+    float* dtab_all = reinterpret_cast<float*>(smem + S * per);
+
+    for (int i = threadIdx.x; i < S * per; i += kThreads) lut[i] = g_lut[slot][i];
+    float z[S][kFastJ];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int j = 0; j < kFastJ; ++j) z[s][j] = g_lut_z[slot][s * kFastJ + j];
+    __syncthreads();
+
+    const int lpb = 1 << lpb_log2;
+    const int li = (int)(threadIdx.x & (lpb - 1));
+    const int lane = (int)(threadIdx.x & 63);
+    const int lane_base = lane - li;
+    const int blocks_per_wg = kThreads >> lpb_log2;
+    float* dtab = dtab_all + (threadIdx.x >> lpb_log2) * (S * kFastJ * L);
+    const int64_t ntiles = (nb + blocks_per_wg - 1) / blocks_per_wg;
+
+    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        const int64_t gb = tile * blocks_per_wg + (threadIdx.x >> lpb_log2);
+        const bool valid = gb < nb;
+        const int64_t off = (valid ? gb : 0) * (int64_t)block + (int64_t)li * kV;
+
+        float xv[kV];
+        if (valid) load16<T>(x + off, xv);
+        else {
+#pragma unroll
+            for (int i = 0; i < kV; ++i) xv[i] = 0.f;
+        }
+        uint32_t mb = 0;
+#pragma unroll
+        for (int i = 0; i < kV; ++i) {
+            uint32_t b = f2bits(xv[i]) & 0x7fffffffu;
+            mb = mb > b ? mb : b;
+        }
+        const float amax = bits2f(group_max_bits(mb, lpb));
+
+        float l1[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) l1[s] = scale_quant<T>(T::round(amax / p.em[s]), p.sf);
+
+        // per-block magnitudes R_T(R_T(level * l2_j) * l1_s)
+        for (int e = li; e < S * kFastJ * L; e += lpb) {
+            const int s = e / (kFastJ * L), j = (e / L) % kFastJ, c = e % L;
+            const int ef = c >> M, mf = c & ((1 << M) - 1);
+            const float v = ef == 0 ? (float)mf * (1.0f / (float)(1 << M))
+                                    : (1.0f + (float)mf * (1.0f / (float)(1 << M))) * pow2f(ef - 1);
+            const float l2 = j < p.J ? p.l2[j][s] : 1.0f;
+            dtab[e] = T::round(T::round(v * l2) * (s == 0 ? l1[0] : l1[S - 1]));
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+
+        float xa[kV];
+#pragma unroll
+        for (int i = 0; i < kV; ++i) xa[i] = fabsf(xv[i]);
+
+        uint32_t ent[S][kV];
+        float tq[S][kV];
+        int jsel[S][NSUBL];
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const float rl1 = 1.0f / l1[s];
+#pragma unroll
+            for (int i = 0; i < kV; ++i) {
+                const float t = div_T<T>(xa[i], l1[s], rl1);
+                tq[s][i] = t;
+                int k = (int)bits_of<T>(t) - (int)p.lo_bits + 1;
+                k = k < 0 ? 0 : (k > p.n + 1 ? p.n + 1 : k);
+                ent[s][i] = lut[s * per + k];
+            }
+            float best[NSUBL];
+#pragma unroll
+            for (int j = 0; j < kFastJ; ++j) {
+                if (j >= p.J) break;
+                const float* dj = dtab + (s * kFastJ + j) * L;
+#pragma unroll
+                for (int sb = 0; sb < NSUBL; ++sb) {
+                    constexpr int n = L2B <= kV ? L2B : kV;
+                    float acc = 0.f;
+#pragma unroll
+                    for (int i = 0; i < n; ++i) {
+                        const float d = dj[(ent[s][sb * n + i] >> (8 * j)) & 0xffu];
+                        const float e = T::round(xa[sb * n + i] - d);
+                        acc += T::round(e * e);
+                    }
+                    if (LPS > 1) {
+                        const int first = lane - (li % LPS);
+                        float tot = __shfl(acc, first, 64);
+                        for (int k2 = 1; k2 < LPS; ++k2) tot += __shfl(acc, first + k2, 64);
+                        acc = tot;
+                    }
+                    const float sse = T::round(acc);
+                    if (j == 0 || better(sse, best[sb])) {
+                        best[sb] = sse;
+                        jsel[s][sb] = j;
+                    }
+                }
+            }
+        }
+
+        // selected candidate per scheme
+        float msel[S][kV];
+        uint32_t lsel[S][kV];
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int i = 0; i < kV; ++i) {
+                constexpr int n = L2B <= kV ? L2B : kV;
+                const int j = jsel[s][i / n];
+                const uint32_t lev = (ent[s][i] >> (8 * j)) & 0xffu;
+                lsel[s][i] = lev;
+                msel[s][i] = dtab[(s * kFastJ + j) * L + lev];
+            }
+        int sstar = 0;
+        if constexpr (S == 2) {
+            float sq0[kV], sq1[kV];
+#pragma unroll
+            for (int i = 0; i < kV; ++i) {
+                const float e0 = T::round(xa[i] - msel[0][i]);
+                const float e1 = T::round(xa[i] - msel[S - 1][i]);
+                sq0[i] = T::round(e0 * e0);
+                sq1[i] = T::round(e1 * e1);
+            }
+            const float s0 = T::round(block_row_sum(sq0, li, lpb, lane_base));
+            const float s1 = T::round(block_row_sum(sq1, li, lpb, lane_base));
+            sstar = better(s1, s0) ? 1 : 0;
+        }
+
+        float out[kV];
+        uint32_t cout[kV];
+#pragma unroll
+        for (int i = 0; i < kV; ++i) {
+            constexpr int n = L2B <= kV ? L2B : kV;
+            const int s = (S == 2 && sstar) ? S - 1 : 0;
+            const int j = jsel[s][i / n];
+            float zj = z[s][0];
+#pragma unroll
+            for (int jj = 1; jj < kFastJ; ++jj) zj = j == jj ? z[s][jj] : zj;
+            const bool neg = (f2bits(xv[i]) >> 31) && tq[s][i] >= zj;
+            const float m = (S == 2 && sstar) ? msel[S - 1][i] : msel[0][i];
+            out[i] = neg ? -m : m;
+            const uint32_t lev = (S == 2 && sstar) ? lsel[S - 1][i] : lsel[0][i];
+            cout[i] = lev | ((neg ? 1u : 0u) << (M + 2));
+        }
+        if (valid) {
+            store16<T>(y + off, out);
+            const int64_t row = gb * (int64_t)block / cols;
+            const int64_t c0 = gb * (int64_t)block - row * cols + (int64_t)li * kV;
+            store_codes<M>(codes, row, cols, c0, cout, false);
+            if (li == 0) {
+                if (l1_out) l1_out[gb] = T::store((S == 2 && sstar) ? l1[S - 1] : l1[0]);
+                if (sch_out) sch_out[gb] = (uint8_t)sstar;
+            }
+            if (l2i_out) {
+                const int nsub_blk = block / L2B;
+                const int s = (S == 2 && sstar) ? S - 1 : 0;
+                if (L2B <= kV) {
+#pragma unroll
+                    for (int sb = 0; sb < NSUBL; ++sb)
+                        l2i_out[gb * nsub_blk + (li * kV) / L2B + sb] = (uint8_t)jsel[s][sb];
+                } else if ((li % LPS) == 0) {
+                    l2i_out[gb * nsub_blk + (li * kV) / L2B] = (uint8_t)jsel[s][0];
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host side: table cache and dispatch
+// ---------------------------------------------------------------------------
+namespace {
+
+struct LutKey {
+    int dtype, mbit, scheme, l2_sc_bit;
+    bool operator==(const LutKey& o) const {
+        return dtype == o.dtype && mbit == o.mbit && scheme == o.scheme && l2_sc_bit == o.l2_sc_bit;
+    }
+};
+
+constexpr int kMaxDevices = 64;
+std::mutex g_mu;
+LutKey g_keys[kMaxDevices][kLutSlots];
+int g_state[kMaxDevices][kLutSlots];    // 0 empty, 1 ready, -1 unusable
+int g_next[kMaxDevices];
+int g_cus[kMaxDevices];
+
+template <class T, int M>
+int build_slot(int slot, const FastParams& p, hipStream_t st) {
+    hipLaunchKernelGGL((build_lut_kernel<T, M>), dim3(64), dim3(256), 0, st, slot, p);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return hbq_fail(HBQ_ERR_HIP, "HBQ level table build failed: %s", hipGetErrorString(e));
+    int status = -1;
+    e = hipMemcpyFromSymbol(&status, HIP_SYMBOL(g_lut_status), sizeof(int), sizeof(int) * slot,
+                            hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hbq_fail(HBQ_ERR_HIP, "HBQ level table status read failed: %s", hipGetErrorString(e));
+    return status;   // 0 ready, > 0 the table shape does not fit this configuration
+}
+
+template <class T, int M, int L2B, int S>
+int launch_fast(const void* x, void* y, void* l1, void* l2i, void* sch, void* codes, int64_t cols, int block,
+                int lpb_log2, int64_t nb, int slot, const FastParams& p, int dev, hipStream_t st) {
+    using St = typename T::storage;
+    const size_t lds = (size_t)S * (p.n + 2) * 4 + (size_t)(kThreads >> lpb_log2) * S * kFastJ * (1 << (M + 2)) * 4;
+    if (lds > 160 * 1024) return 0;
+    auto kern = hbq_fast_kernel<T, M, L2B, S>;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kThreads, lds) != hipSuccess || per_cu <= 0)
+        return 0;
+    const int64_t blocks_per_wg = kThreads >> lpb_log2;
+    const int64_t ntiles = (nb + blocks_per_wg - 1) / blocks_per_wg;
+    int64_t grid = (int64_t)g_cus[dev] * per_cu;
+    if (grid > ntiles) grid = ntiles;
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), lds, st, (const St*)x, (St*)y, (St*)l1,
+                       (uint8_t*)l2i, (uint8_t*)sch, (uint8_t*)codes, cols, block, lpb_log2, nb, slot, p);
+    return 1;
+}
+
+template <class T, int M>
+int fast_by_shape(int l2b, int S, const void* x, void* y, void* l1, void* l2i, void* sch, void* codes, int64_t cols,
+                  int block, int lpb_log2, int64_t nb, int slot, const FastParams& p, int dev, hipStream_t st) {
+#define FAST_CASE(LB, SS)                                                                                   \
+    if (l2b == LB && S == SS)                                                                               \
+        return launch_fast<T, M, LB, SS>(x, y, l1, l2i, sch, codes, cols, block, lpb_log2, nb, slot, p, dev, st);
+    FAST_CASE(8, 1) FAST_CASE(8, 2) FAST_CASE(16, 1) FAST_CASE(16, 2) FAST_CASE(32, 1) FAST_CASE(32, 2)
+#undef FAST_CASE
+    return 0;
+}
+
+}  // namespace
+}  // namespace hbq
+
+using namespace hbq;
+
+int hbq_fast_try(const void* x, void* y, void* l1, void* l2i, void* sch, void* codes, int64_t rows, int64_t cols,
+                 int dtype, int block, int mbit, int l2b, int l2_sc_bit, int scheme, const HbqParams& hp,
+                 hipStream_t st) {
+    if (dtype != kF16 && dtype != kBF16) return 0;
+    if (mbit < 1 || mbit > 3 || hp.J > kFastJ) return 0;
+    if (l2b != 8 && l2b != 16 && l2b != 32) return 0;
+    int lb = 0;
+    while ((1 << lb) < block) ++lb;
+    if ((1 << lb) != block || block < 64 || block > 1024 || block % l2b) return 0;
+    if (cols % block || ((uintptr_t)x % 16) || ((uintptr_t)y % 16) || (codes && ((uintptr_t)codes % 16))) return 0;
+    const int S = scheme == 7 ? 2 : 1;
+
+    // table range [2^lo, 2^hi): below 2^-(m+2) every candidate rounds to level 0 (l2 >= 1);
+    // at or above 8 * max(l2) every candidate saturates
+    float l2max = 1.f;
+    for (int s = 0; s < S; ++s)
+        for (int j = 0; j < hp.J; ++j) l2max = hp.l2[j][s] > l2max ? hp.l2[j][s] : l2max;
+    int hi = 3;
+    while ((float)(1 << (hi - 3)) < l2max) ++hi;
+    const int lo = -(mbit + 2);
+    if (hi - lo > kLutMaxBinades) return 0;
+    FastParams p{};
+    p.S = S;
+    p.J = hp.J;
+    p.L = 1 << (mbit + 2);
+    const int mbits_T = dtype == kF16 ? 10 : 7;
+    const int bias = dtype == kF16 ? 15 : 127;
+    p.n = (hi - lo) << mbits_T;
+    p.lo_bits = (uint32_t)(bias + lo) << mbits_T;
+    for (int j = 0; j < kFastJ; ++j)
+        for (int s = 0; s < 2; ++s) p.l2[j][s] = j < hp.J ? hp.l2[j][s] : 1.f;
+    p.em[0] = hp.em[0];
+    p.em[1] = hp.em[S - 1];
+    p.sf = hp.sf;
+
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+    int slot = -1;
+    {
+        std::lock_guard<std::mutex> g(g_mu);
+        if (g_cus[dev] == 0) {
+            int cus = 0;
+            if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+                return 0;
+            g_cus[dev] = cus;
+        }
+        const LutKey key{dtype, mbit, scheme, l2_sc_bit};
+        for (int i = 0; i < kLutSlots; ++i)
+            if (g_state[dev][i] != 0 && g_keys[dev][i] == key) slot = i;
+        if (slot >= 0 && g_state[dev][slot] < 0) return 0;
+        if (slot < 0) {
+            slot = g_next[dev];
+            g_next[dev] = (g_next[dev] + 1) % kLutSlots;
+            g_keys[dev][slot] = key;
+            int rc;
+            if (dtype == kF16)
+                rc = mbit == 1 ? build_slot<F16, 1>(slot, p, st) : mbit == 2 ? build_slot<F16, 2>(slot, p, st)
+                                                                               : build_slot<F16, 3>(slot, p, st);
+            else
+                rc = mbit == 1 ? build_slot<BF16, 1>(slot, p, st) : mbit == 2 ? build_slot<BF16, 2>(slot, p, st)
+                                                                                : build_slot<BF16, 3>(slot, p, st);
+            if (rc < 0 || rc == HBQ_ERR_HIP) {
+                g_state[dev][slot] = 0;
+                return -HBQ_ERR_HIP;
+            }
+            g_state[dev][slot] = rc == 0 ? 1 : -1;
+            if (rc != 0) return 0;
+        }
+    }
+    const int64_t nb = rows * (cols / block);
+    if (nb == 0) return 1;
+    const int lpb_log2 = lb - 4;
+    int done;
+#define FAST_T(TT)                                                                                              \
+    (mbit == 1 ? fast_by_shape<TT, 1>(l2b, S, x, y, l1, l2i, sch, codes, cols, block, lpb_log2, nb, slot, p, dev, st) \
+     : mbit == 2 ? fast_by_shape<TT, 2>(l2b, S, x, y, l1, l2i, sch, codes, cols, block, lpb_log2, nb, slot, p, dev, st) \
+                 : fast_by_shape<TT, 3>(l2b, S, x, y, l1, l2i, sch, codes, cols, block, lpb_log2, nb, slot, p, dev, st))
+    done = dtype == kF16 ? FAST_T(F16) : FAST_T(BF16);
+#undef FAST_T
+    return done;
+}

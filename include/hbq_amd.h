@@ -53,6 +53,10 @@ const char *hbq_last_error(void);
 /* ABI revision of this header. */
 int hbq_abi_version(void);
 
+/* No reference counterpart: a test hook.  on != 0 routes every hbq_hbq_qdq call
+ * to the generic kernel instead of the table-driven one; returns the old setting. */
+int hbq_set_generic_only(int on);
+
 /*
  * MXFP / NVFP quantize-dequantize.
  * Replaces MXFPQuantizer.q (src/quantizer.py:513-539) together with

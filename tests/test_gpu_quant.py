@@ -237,3 +237,25 @@ def test_hbq_3d_input(gpu, oracle):
     assert y.shape == x.shape and q.shared_scale.shape == (6, 32, 2) and q.l2_scale.shape == (6, 32, 2, 16)
     ref = oracle.hbq_qdq(to_bits(x.view(-1, 256)), "f16", block_size=128, **HBQCFG["hbq_kv4"])
     assert mismatches(to_bits(y.view(-1, 256)), ref["y"], "f16") == 0
+
+
+@pytest.mark.parametrize("name", ["hbq_a_act", "hbq_a_wgt", "hbq_e_act", "hbq_e_wgt", "hbq_kv4", "hbq_a_wgt_ceil"])
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_hbq_table_kernel_equals_generic(gpu, name, dt):
+    """The table-driven kernel and the generic kernel agree bit for bit, codes and scales included."""
+    from hbq_amd import _lib
+    print(f"fast vs generic {name} {dt}", flush=True)
+    x = _edge_rows(synth(512, 4096, 17, dt)).to(gpu)
+    q = _hbq(HBQCFG[name])
+    fast = q.quantize(x)
+    old = _lib.lib().hbq_set_generic_only(1)
+    try:
+        gen = q.quantize(x)
+    finally:
+        _lib.lib().hbq_set_generic_only(old)
+    assert mismatches(to_bits(fast.y), to_bits(gen.y), dt) == 0
+    ok = ~torch.isnan(fast.y)          # codes of NaN outputs are unspecified
+    per_byte = ok if q.mbit != 1 else ok.view(ok.shape[0], -1, 2).all(-1)
+    assert torch.equal(fast.codes[per_byte], gen.codes[per_byte])
+    assert mismatches(to_bits(fast.scales), to_bits(gen.scales), dt) == 0
+    assert torch.equal(fast.l2_index, gen.l2_index) and torch.equal(fast.scheme, gen.scheme)
