@@ -20,6 +20,7 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <mutex>
+#include <type_traits>
 #include <stdint.h>
 #include <string.h>
 
@@ -50,8 +51,10 @@ struct FastParams {
     ScaleFmt sf;
 };
 
+// bit pattern of a value already representable in T
 template <class T>
 __device__ __forceinline__ uint32_t bits_of(float v) {
+    if (T::dt == kBF16) return f2bits(v) >> 16;
     return (uint32_t)T::store(v);
 }
 
@@ -105,37 +108,59 @@ __global__ void build_lut_kernel(int slot, FastParams p) {
     }
 }
 
-template <class T, int M, int L2B, int S>
+// Per-block magnitude tables live in a per-wave LDS region laid out
+// [scheme][candidate][level][block-in-wave], so the lanes of different blocks
+// reading the same (scheme, candidate) row hit different banks.
+template <int S, int L>
+__device__ __forceinline__ int dtab_index(int s, int j, int lev, int bw, int bpw) {
+    return ((s * kFastJ + j) * L + lev) * bpw + bw;
+}
+
+// fp16 tables hold halves (the candidate errors are computed in packed fp16),
+// other dtypes hold floats
+template <class T>
+using DTabT = typename std::conditional<T::dt == kF16, _Float16, float>::type;
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+template <class T, int M, int L2B, int S, int LPB_LOG2>
 __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::storage* __restrict__ x,
                                                             typename T::storage* __restrict__ y,
                                                             typename T::storage* __restrict__ l1_out,
                                                             uint8_t* __restrict__ l2i_out,
                                                             uint8_t* __restrict__ sch_out,
-                                                            uint8_t* __restrict__ codes, int64_t cols, int block,
-                                                            int lpb_log2, int64_t nb, int slot, FastParams p) {
+                                                            uint8_t* __restrict__ codes, int64_t nb, int slot,
+                                                            FastParams p) {
+    constexpr int lpb_log2 = LPB_LOG2;
+    constexpr int block = kV << LPB_LOG2;
     constexpr int L = 1 << (M + 2);
     constexpr int NSUBL = L2B <= kV ? kV / L2B : 1;
     constexpr int LPS = L2B <= kV ? 1 : L2B / kV;
+    constexpr int SUBN = L2B <= kV ? L2B : kV;          // elements of one sub-block held by a lane
     extern __shared__ uint32_t smem[];
     const int per = p.n + 2;
     uint32_t* lut = smem;
-    float* dtab_all = reinterpret_cast<float*>(smem + S * per);
 
     for (int i = threadIdx.x; i < S * per; i += kThreads) lut[i] = g_lut[slot][i];
-    float z[S][kFastJ];
+    float z[S][kFastJ], l2v[S][kFastJ];
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
-        for (int j = 0; j < kFastJ; ++j) z[s][j] = g_lut_z[slot][s * kFastJ + j];
+        for (int j = 0; j < kFastJ; ++j) {
+            z[s][j] = g_lut_z[slot][s * kFastJ + j];
+            l2v[s][j] = p.l2[j][s];
+        }
     __syncthreads();
 
-    const int lpb = 1 << lpb_log2;
+    constexpr int lpb = 1 << lpb_log2;
     const int li = (int)(threadIdx.x & (lpb - 1));
     const int lane = (int)(threadIdx.x & 63);
     const int lane_base = lane - li;
-    const int blocks_per_wg = kThreads >> lpb_log2;
-    float* dtab = dtab_all + (threadIdx.x >> lpb_log2) * (S * kFastJ * L);
+    constexpr int bpw = 64 >> lpb_log2;                   // blocks per wave
+    const int bw = lane >> lpb_log2;                      // block index within the wave
+    DTabT<T>* dtab = reinterpret_cast<DTabT<T>*>(smem + S * per) + (threadIdx.x >> 6) * (S * kFastJ * L * bpw);
+    constexpr int blocks_per_wg = kThreads >> lpb_log2;
     const int64_t ntiles = (nb + blocks_per_wg - 1) / blocks_per_wg;
+    const float tiny = T::dt == kF16 ? 6.103515625e-05f : 1.17549435e-38f;
 
     for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
         const int64_t gb = tile * blocks_per_wg + (threadIdx.x >> lpb_log2);
@@ -149,9 +174,11 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
             for (int i = 0; i < kV; ++i) xv[i] = 0.f;
         }
         uint32_t mb = 0;
+        float xa[kV];
 #pragma unroll
         for (int i = 0; i < kV; ++i) {
-            uint32_t b = f2bits(xv[i]) & 0x7fffffffu;
+            xa[i] = fabsf(xv[i]);
+            const uint32_t b = f2bits(xa[i]);
             mb = mb > b ? mb : b;
         }
         const float amax = bits2f(group_max_bits(mb, lpb));
@@ -160,33 +187,47 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
 #pragma unroll
         for (int s = 0; s < S; ++s) l1[s] = scale_quant<T>(T::round(amax / p.em[s]), p.sf);
 
-        // per-block magnitudes R_T(R_T(level * l2_j) * l1_s)
-        for (int e = li; e < S * kFastJ * L; e += lpb) {
-            const int s = e / (kFastJ * L), j = (e / L) % kFastJ, c = e % L;
+        // magnitudes R_T(R_T(level * l2_j) * l1_s) of this block
+        for (int c = li; c < L; c += lpb) {
             const int ef = c >> M, mf = c & ((1 << M) - 1);
             const float v = ef == 0 ? (float)mf * (1.0f / (float)(1 << M))
                                     : (1.0f + (float)mf * (1.0f / (float)(1 << M))) * pow2f(ef - 1);
-            const float l2 = j < p.J ? p.l2[j][s] : 1.0f;
-            dtab[e] = T::round(T::round(v * l2) * (s == 0 ? l1[0] : l1[S - 1]));
-        }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-
-        float xa[kV];
 #pragma unroll
-        for (int i = 0; i < kV; ++i) xa[i] = fabsf(xv[i]);
+            for (int s = 0; s < S; ++s)
+#pragma unroll
+                for (int j = 0; j < kFastJ; ++j)
+                    dtab[dtab_index<S, L>(s, j, c, bw, bpw)] = (DTabT<T>)T::round(T::round(v * l2v[s][j]) * l1[s]);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
+        h2_t xp[kV / 2];
+        if constexpr (T::dt == kF16) {
+#pragma unroll
+            for (int i = 0; i < kV; i += 2) xp[i / 2] = (h2_t){(_Float16)xa[i], (_Float16)xa[i + 1]};
+        }
         uint32_t ent[S][kV];
         float tq[S][kV];
         int jsel[S][NSUBL];
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             const float rl1 = 1.0f / l1[s];
+            bool exact = false;
+#pragma unroll
+            for (int i = 0; i < kV; i += 2) {
+                const float q0 = xa[i] * rl1, q1 = xa[i + 1] * rl1;
+                exact |= (q0 < tiny) | (q1 < tiny);
+                round2<T>(q0, q1, tq[s][i], tq[s][i + 1]);
+            }
+            if (exact) {   // quotients in T's subnormal range can be exact ties: divide
+#pragma unroll
+                for (int i = 0; i < kV; ++i)
+                    if (xa[i] * rl1 < tiny) tq[s][i] = T::round(xa[i] / l1[s]);
+            }
 #pragma unroll
             for (int i = 0; i < kV; ++i) {
-                const float t = div_T<T>(xa[i], l1[s], rl1);
-                tq[s][i] = t;
-                int k = (int)bits_of<T>(t) - (int)p.lo_bits + 1;
+                int k = (int)bits_of<T>(tq[s][i]) - (int)p.lo_bits + 1;
                 k = k < 0 ? 0 : (k > p.n + 1 ? p.n + 1 : k);
                 ent[s][i] = lut[s * per + k];
             }
@@ -194,16 +235,31 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
 #pragma unroll
             for (int j = 0; j < kFastJ; ++j) {
                 if (j >= p.J) break;
-                const float* dj = dtab + (s * kFastJ + j) * L;
 #pragma unroll
                 for (int sb = 0; sb < NSUBL; ++sb) {
-                    constexpr int n = L2B <= kV ? L2B : kV;
                     float acc = 0.f;
 #pragma unroll
-                    for (int i = 0; i < n; ++i) {
-                        const float d = dj[(ent[s][sb * n + i] >> (8 * j)) & 0xffu];
-                        const float e = T::round(xa[sb * n + i] - d);
-                        acc += T::round(e * e);
+                    for (int i = sb * SUBN; i < (sb + 1) * SUBN; i += 2) {
+                        const int lv0 = (int)((ent[s][i] >> (8 * j)) & 0xffu);
+                        const int lv1 = (int)((ent[s][i + 1] >> (8 * j)) & 0xffu);
+                        if constexpr (T::dt == kF16) {
+                            // R16(|x| - d) and R16(e^2) are single correctly rounded fp16 ops
+                            const h2_t dp = {dtab[dtab_index<S, L>(s, j, lv0, bw, bpw)],
+                                             dtab[dtab_index<S, L>(s, j, lv1, bw, bpw)]};
+                            const h2_t e = xp[i / 2] - dp;
+                            h2_t q = e * e;
+                            asm("" : "+v"(q));
+                            acc += (float)q.x;
+                            acc += (float)q.y;
+                        } else {
+                            const float d0 = dtab[dtab_index<S, L>(s, j, lv0, bw, bpw)];
+                            const float d1 = dtab[dtab_index<S, L>(s, j, lv1, bw, bpw)];
+                            float e0, e1, q0, q1;
+                            round2<T>(xa[i] - d0, xa[i + 1] - d1, e0, e1);
+                            round2<T>(e0 * e0, e1 * e1, q0, q1);
+                            acc += q0;
+                            acc += q1;
+                        }
                     }
                     if (LPS > 1) {
                         const int first = lane - (li % LPS);
@@ -220,28 +276,28 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
             }
         }
 
-        // selected candidate per scheme
+        // the selected candidate of every scheme
         float msel[S][kV];
         uint32_t lsel[S][kV];
 #pragma unroll
         for (int s = 0; s < S; ++s)
 #pragma unroll
             for (int i = 0; i < kV; ++i) {
-                constexpr int n = L2B <= kV ? L2B : kV;
-                const int j = jsel[s][i / n];
+                const int j = jsel[s][i / SUBN];
                 const uint32_t lev = (ent[s][i] >> (8 * j)) & 0xffu;
                 lsel[s][i] = lev;
-                msel[s][i] = dtab[(s * kFastJ + j) * L + lev];
+                msel[s][i] = (float)dtab[dtab_index<S, L>(s, j, (int)lev, bw, bpw)];
             }
         int sstar = 0;
         if constexpr (S == 2) {
             float sq0[kV], sq1[kV];
 #pragma unroll
-            for (int i = 0; i < kV; ++i) {
-                const float e0 = T::round(xa[i] - msel[0][i]);
-                const float e1 = T::round(xa[i] - msel[S - 1][i]);
-                sq0[i] = T::round(e0 * e0);
-                sq1[i] = T::round(e1 * e1);
+            for (int i = 0; i < kV; i += 2) {
+                float a0, a1, b0, b1;
+                round2<T>(xa[i] - msel[0][i], xa[i + 1] - msel[0][i + 1], a0, a1);
+                round2<T>(a0 * a0, a1 * a1, sq0[i], sq0[i + 1]);
+                round2<T>(xa[i] - msel[S - 1][i], xa[i + 1] - msel[S - 1][i + 1], b0, b1);
+                round2<T>(b0 * b0, b1 * b1, sq1[i], sq1[i + 1]);
             }
             const float s0 = T::round(block_row_sum(sq0, li, lpb, lane_base));
             const float s1 = T::round(block_row_sum(sq1, li, lpb, lane_base));
@@ -250,25 +306,46 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
 
         float out[kV];
         uint32_t cout[kV];
+        float zsel[NSUBL];
+#pragma unroll
+        for (int sb = 0; sb < NSUBL; ++sb) {
+            const int s = (S == 2 && sstar) ? S - 1 : 0;
+            const int j = jsel[s][sb];
+            float zz = z[s][0];
+#pragma unroll
+            for (int jj = 1; jj < kFastJ; ++jj) zz = j == jj ? z[s][jj] : zz;
+            zsel[sb] = zz;
+        }
 #pragma unroll
         for (int i = 0; i < kV; ++i) {
-            constexpr int n = L2B <= kV ? L2B : kV;
-            const int s = (S == 2 && sstar) ? S - 1 : 0;
-            const int j = jsel[s][i / n];
-            float zj = z[s][0];
-#pragma unroll
-            for (int jj = 1; jj < kFastJ; ++jj) zj = j == jj ? z[s][jj] : zj;
-            const bool neg = (f2bits(xv[i]) >> 31) && tq[s][i] >= zj;
-            const float m = (S == 2 && sstar) ? msel[S - 1][i] : msel[0][i];
+            const bool s1 = S == 2 && sstar;
+            const float t = s1 ? tq[S - 1][i] : tq[0][i];
+            const bool neg = (f2bits(xv[i]) >> 31) && t >= zsel[i / SUBN];
+            const float m = s1 ? msel[S - 1][i] : msel[0][i];
             out[i] = neg ? -m : m;
-            const uint32_t lev = (S == 2 && sstar) ? lsel[S - 1][i] : lsel[0][i];
+            const uint32_t lev = s1 ? lsel[S - 1][i] : lsel[0][i];
             cout[i] = lev | ((neg ? 1u : 0u) << (M + 2));
         }
         if (valid) {
             store16<T>(y + off, out);
-            const int64_t row = gb * (int64_t)block / cols;
-            const int64_t c0 = gb * (int64_t)block - row * cols + (int64_t)li * kV;
-            store_codes<M>(codes, row, cols, c0, cout, false);
+            if (codes) {
+                if constexpr (M == 1) {
+                    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        w0 |= (cout[i] & 0xfu) << (4 * i);
+                        w1 |= (cout[8 + i] & 0xfu) << (4 * i);
+                    }
+                    *reinterpret_cast<uint2*>(codes + off / 2) = make_uint2(w0, w1);
+                } else {
+                    uint32_t w[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        w[i] = (cout[4 * i] & 0xffu) | ((cout[4 * i + 1] & 0xffu) << 8) |
+                               ((cout[4 * i + 2] & 0xffu) << 16) | ((cout[4 * i + 3] & 0xffu) << 24);
+                    *reinterpret_cast<uint4*>(codes + off) = make_uint4(w[0], w[1], w[2], w[3]);
+                }
+            }
             if (li == 0) {
                 if (l1_out) l1_out[gb] = T::store((S == 2 && sstar) ? l1[S - 1] : l1[0]);
                 if (sch_out) sch_out[gb] = (uint8_t)sstar;
@@ -285,6 +362,7 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
                 }
             }
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
     }
 }
@@ -321,13 +399,15 @@ int build_slot(int slot, const FastParams& p, hipStream_t st) {
     return status;   // 0 ready, > 0 the table shape does not fit this configuration
 }
 
-template <class T, int M, int L2B, int S>
-int launch_fast(const void* x, void* y, void* l1, void* l2i, void* sch, void* codes, int64_t cols, int block,
-                int lpb_log2, int64_t nb, int slot, const FastParams& p, int dev, hipStream_t st) {
+template <class T, int M, int L2B, int S, int LPB_LOG2>
+int launch_fast_b(const void* x, void* y, void* l1, void* l2i, void* sch, void* codes, int64_t nb, int slot,
+                  const FastParams& p, int dev, hipStream_t st) {
+    constexpr int lpb_log2 = LPB_LOG2;
     using St = typename T::storage;
-    const size_t lds = (size_t)S * (p.n + 2) * 4 + (size_t)(kThreads >> lpb_log2) * S * kFastJ * (1 << (M + 2)) * 4;
+    const size_t lds = (size_t)S * (p.n + 2) * 4 +
+                       (size_t)(kThreads >> lpb_log2) * S * kFastJ * (1 << (M + 2)) * sizeof(DTabT<T>);
     if (lds > 160 * 1024) return 0;
-    auto kern = hbq_fast_kernel<T, M, L2B, S>;
+    auto kern = hbq_fast_kernel<T, M, L2B, S, LPB_LOG2>;
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kThreads, lds) != hipSuccess || per_cu <= 0)
         return 0;
@@ -336,8 +416,18 @@ int launch_fast(const void* x, void* y, void* l1, void* l2i, void* sch, void* co
     int64_t grid = (int64_t)g_cus[dev] * per_cu;
     if (grid > ntiles) grid = ntiles;
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), lds, st, (const St*)x, (St*)y, (St*)l1,
-                       (uint8_t*)l2i, (uint8_t*)sch, (uint8_t*)codes, cols, block, lpb_log2, nb, slot, p);
+                       (uint8_t*)l2i, (uint8_t*)sch, (uint8_t*)codes, nb, slot, p);
     return 1;
+}
+
+template <class T, int M, int L2B, int S>
+int launch_fast(const void* x, void* y, void* l1, void* l2i, void* sch, void* codes, int64_t cols, int block,
+                int lpb_log2, int64_t nb, int slot, const FastParams& p, int dev, hipStream_t st) {
+    (void)cols;
+    (void)block;
+    // block 128 (the HBQ configurations); other block sizes take the generic kernel
+    if (lpb_log2 == 3) return launch_fast_b<T, M, L2B, S, 3>(x, y, l1, l2i, sch, codes, nb, slot, p, dev, st);
+    return 0;
 }
 
 template <class T, int M>
@@ -364,7 +454,7 @@ int hbq_fast_try(const void* x, void* y, void* l1, void* l2i, void* sch, void* c
     if (l2b != 8 && l2b != 16 && l2b != 32) return 0;
     int lb = 0;
     while ((1 << lb) < block) ++lb;
-    if ((1 << lb) != block || block < 64 || block > 1024 || block % l2b) return 0;
+    if (block != 128 || block % l2b) return 0;
     if (cols % block || ((uintptr_t)x % 16) || ((uintptr_t)y % 16) || (codes && ((uintptr_t)codes % 16))) return 0;
     const int S = scheme == 7 ? 2 : 1;
 

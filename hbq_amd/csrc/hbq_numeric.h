@@ -40,10 +40,7 @@ struct BF16 {
     static constexpr DType dt = kBF16;
     __device__ __forceinline__ static float load(storage s) { return bits2f((uint32_t)s << 16); }
     __device__ __forceinline__ static storage store(float v) {
-        uint32_t x = f2bits(v);
-        if ((x & 0x7fffffffu) > 0x7f800000u) return (storage)((x >> 16) | 0x40u);
-        x += 0x7fffu + ((x >> 16) & 1u);
-        return (storage)(x >> 16);
+        return __builtin_bit_cast(uint16_t, (__bf16)v);   // v_cvt_pk_bf16_f32: RNE, subnormals kept
     }
     __device__ __forceinline__ static float round(float v) { return load(store(v)); }
 };
@@ -55,6 +52,22 @@ struct F32 {
     __device__ __forceinline__ static storage store(float v) { return v; }
     __device__ __forceinline__ static float round(float v) { return v; }
 };
+
+// Round two floats to T at once (one v_cvt_pk_bf16_f32 for bf16).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+template <class T>
+__device__ __forceinline__ void round2(float a, float b, float& ra, float& rb) {
+    if constexpr (T::dt == kBF16) {
+        const bf16x2_t r = __builtin_convertvector((f32x2_t){a, b}, bf16x2_t);
+        const uint32_t u = __builtin_bit_cast(uint32_t, r);
+        ra = bits2f(u << 16);
+        rb = bits2f(u & 0xffff0000u);
+    } else {
+        ra = T::round(a);
+        rb = T::round(b);
+    }
+}
 
 // ---- binade exponent and the rounded-log2 exponent ------------------------
 // True exponent e of a positive finite float (2^e <= a < 2^(e+1)), subnormals included.
@@ -106,10 +119,11 @@ __device__ __forceinline__ float scale_quant(float s, const ScaleFmt& f) {
     bool under = !f.allow_sub && (a < f.thr) && !is_zero;
     float fe = a == __builtin_inff() ? a : log2_exponent<T>(is_zero ? 1.f : a, 0);
     float e = fe < f.emin ? f.emin : (fe > f.emax ? f.emax : fe);
-    float p2 = T::round(pow2f((int)e));
+    // division by a power of two = multiplication by its exact reciprocal
+    float rp2 = pow2f(-(int)e);
     float sg = s > 0.f ? 1.f : (s < 0.f ? -1.f : 0.f);
-    float mant = sub ? T::round(T::round(s / p2) * f.mshift)
-                     : T::round(T::round(T::round(s / p2) - sg) * f.mshift);
+    float mant = sub ? T::round(T::round(s * rp2) * f.mshift)
+                     : T::round(T::round(T::round(s * rp2) - sg) * f.mshift);
     float mr = f.use_ceil ? ceilf(fabsf(mant)) : floorf(T::round(fabsf(mant) + 0.5f));
     bool overflow = (mr > f.mmax) && (e != f.emax);
     if (mr > f.mmax) mr = f.mmax;
@@ -117,8 +131,9 @@ __device__ __forceinline__ float scale_quant(float s, const ScaleFmt& f) {
     if (overflow) e = e + 1.f;
     float sm = sg * mr;
     float p2b = T::round(pow2f((int)e));
-    float q = sub ? T::round(T::round(sm / f.mshift) * p2b)
-                  : T::round(T::round(T::round(sm / f.mshift) + sg) * p2b);
+    const float rshift = 1.0f / f.mshift;   // exact: mshift is a power of two
+    float q = sub ? T::round(T::round(sm * rshift) * p2b)
+                  : T::round(T::round(T::round(sm * rshift) + sg) * p2b);
     if (is_zero || under) q = 0.f;
     if (f.e4m3) q = q > 448.f ? 448.f : (q < -448.f ? -448.f : q);
     return q;
