@@ -36,10 +36,14 @@ constexpr int kLutMaxEntries = 2 * (kLutMaxBinades * 1024 + 2);
 constexpr int kFastJ = 4;
 
 // level tables: per slot, S schemes of (n + 2) words: [0] below the table range
-// (all levels 0), [1 .. n] the binades [2^lo, 2^hi), [n + 1] at or above 2^hi (saturated)
+// (all levels 0), [1 .. n] the binades [2^lo, 2^hi), [n + 1] at or above 2^hi
+// (saturated).  Byte j of a word is candidate j's level times the element size
+// of the magnitude table, i.e. its byte offset in a table row.
 static __device__ uint32_t g_lut[kLutSlots][kLutMaxEntries];
-// per slot: z[s][j] = smallest t > 0 with R_T(t / l2[j][s]) != 0, then a status word
+// per slot: z[s][j] = smallest t > 0 with R_T(t / l2[j][s]) != 0
 static __device__ float g_lut_z[kLutSlots][2 * kFastJ];
+// per slot: R_T(level value * l2[j][s]) for every level (block independent)
+static __device__ float g_lut_qs[kLutSlots][2][kFastJ][32];
 static __device__ int g_lut_status[kLutSlots];
 
 struct FastParams {
@@ -48,8 +52,14 @@ struct FastParams {
     uint32_t lo_bits;          // T bit pattern of 2^lo
     float l2[kFastJ][2];       // L2 factors
     float em[2];
-    ScaleFmt sf;
+    int use_ceil;
 };
+
+// fp16 tables hold halves (the candidate errors are computed in packed fp16),
+// bf16 tables hold floats
+template <class T>
+using DTabT = typename std::conditional<T::dt == kF16, _Float16, float>::type;
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
 // bit pattern of a value already representable in T
 template <class T>
@@ -71,20 +81,34 @@ __device__ __forceinline__ uint32_t level_of(float u) {
     return c & ((1u << (M + 2)) - 1u);
 }
 
+template <int M>
+__device__ __forceinline__ float level_value(int c) {
+    const int ef = c >> M, mf = c & ((1 << M) - 1);
+    return ef == 0 ? (float)mf * (1.0f / (float)(1 << M))
+                   : (1.0f + (float)mf * (1.0f / (float)(1 << M))) * pow2f(ef - 1);
+}
+
 template <class T, int M>
 __global__ void build_lut_kernel(int slot, FastParams p) {
+    constexpr uint32_t esize = sizeof(DTabT<T>);
     const int per = p.n + 2;
     const int total = p.S * per;
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
         const int s = i / per, k = i % per;
         uint32_t w = 0;
         if (k == per - 1) {
-            for (int j = 0; j < p.J; ++j) w |= ((1u << (M + 2)) - 1u) << (8 * j);
+            for (int j = 0; j < p.J; ++j) w |= (((1u << (M + 2)) - 1u) * esize) << (8 * j);
         } else if (k > 0) {
             const float t = from_bits<T>(p.lo_bits + (uint32_t)(k - 1));
-            for (int j = 0; j < p.J; ++j) w |= level_of<T, M>(T::round(t / p.l2[j][s])) << (8 * j);
+            for (int j = 0; j < p.J; ++j) w |= (level_of<T, M>(T::round(t / p.l2[j][s])) * esize) << (8 * j);
         }
         g_lut[slot][i] = w;
+    }
+    const int g = blockIdx.x * blockDim.x + threadIdx.x;
+    if (g < 2 * kFastJ * 32) {
+        const int s = g / (kFastJ * 32), j = (g / 32) % kFastJ, c = g % 32;
+        const float l2 = (s < p.S && j < p.J) ? p.l2[j][s] : 1.0f;
+        g_lut_qs[slot][s][j][c] = c < (1 << (M + 2)) ? T::round(level_value<M>(c) * l2) : 0.0f;
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         int status = 0;
@@ -108,21 +132,20 @@ __global__ void build_lut_kernel(int slot, FastParams p) {
     }
 }
 
-// Per-block magnitude tables live in a per-wave LDS region laid out
-// [scheme][candidate][level][block-in-wave], so the lanes of different blocks
-// reading the same (scheme, candidate) row hit different banks.
-template <int S, int L>
-__device__ __forceinline__ int dtab_index(int s, int j, int lev, int bw, int bpw) {
-    return ((s * kFastJ + j) * L + lev) * bpw + bw;
+// max over the 8 lanes of a block with DPP: swap neighbours, swap pairs, mirror halves of 8
+__device__ __forceinline__ uint32_t max8_dpp(uint32_t v) {
+    uint32_t o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xf, 0xf, true);   // quad_perm [1,0,3,2]
+    v = v > o ? v : o;
+    o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xf, 0xf, true);            // quad_perm [2,3,0,1]
+    v = v > o ? v : o;
+    o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xf, 0xf, true);           // row_half_mirror
+    return v > o ? v : o;
 }
 
-// fp16 tables hold halves (the candidate errors are computed in packed fp16),
-// other dtypes hold floats
-template <class T>
-using DTabT = typename std::conditional<T::dt == kF16, _Float16, float>::type;
-typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-
-template <class T, int M, int L2B, int S, int LPB_LOG2>
+// Block 128 (8 lanes x 16 elements).  Per-wave magnitude tables, laid out
+// [scheme][candidate][block-in-wave][level] with rows padded by one entry so
+// that the eight blocks of a wave fall on different LDS banks.
+template <class T, int M, int L2B, int S>
 __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::storage* __restrict__ x,
                                                             typename T::storage* __restrict__ y,
                                                             typename T::storage* __restrict__ l1_out,
@@ -130,74 +153,99 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
                                                             uint8_t* __restrict__ sch_out,
                                                             uint8_t* __restrict__ codes, int64_t nb, int slot,
                                                             FastParams p) {
-    constexpr int lpb_log2 = LPB_LOG2;
-    constexpr int block = kV << LPB_LOG2;
+    using DT = DTabT<T>;
+    constexpr int lpb = 8;
+    constexpr int bpw = 64 / lpb;
+    constexpr int block = kV * lpb;
     constexpr int L = 1 << (M + 2);
+    constexpr int ROW = L + 1;                            // padded row (entries)
     constexpr int NSUBL = L2B <= kV ? kV / L2B : 1;
     constexpr int LPS = L2B <= kV ? 1 : L2B / kV;
-    constexpr int SUBN = L2B <= kV ? L2B : kV;          // elements of one sub-block held by a lane
+    constexpr int SUBN = L2B <= kV ? L2B : kV;
+    constexpr int blocks_per_wg = kThreads / lpb;
     extern __shared__ uint32_t smem[];
     const int per = p.n + 2;
     uint32_t* lut = smem;
 
     for (int i = threadIdx.x; i < S * per; i += kThreads) lut[i] = g_lut[slot][i];
-    float z[S][kFastJ], l2v[S][kFastJ];
+    const int li = (int)(threadIdx.x & (lpb - 1));
+    const int lane = (int)(threadIdx.x & 63);
+    const int lane_base = lane - li;
+    const int bw = lane / lpb;
+
+    float z[S][kFastJ];
+    // this lane builds levels c = li and li + 8 (L = 16) of every (scheme, candidate) row
+    constexpr int CPL = (L + lpb - 1) / lpb;
+    float qs[S][kFastJ][CPL];
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
         for (int j = 0; j < kFastJ; ++j) {
             z[s][j] = g_lut_z[slot][s * kFastJ + j];
-            l2v[s][j] = p.l2[j][s];
+#pragma unroll
+            for (int k = 0; k < CPL; ++k) qs[s][j][k] = g_lut_qs[slot][s][j][(li + k * lpb) & 31];
         }
     __syncthreads();
 
-    constexpr int lpb = 1 << lpb_log2;
-    const int li = (int)(threadIdx.x & (lpb - 1));
-    const int lane = (int)(threadIdx.x & 63);
-    const int lane_base = lane - li;
-    constexpr int bpw = 64 >> lpb_log2;                   // blocks per wave
-    const int bw = lane >> lpb_log2;                      // block index within the wave
-    DTabT<T>* dtab = reinterpret_cast<DTabT<T>*>(smem + S * per) + (threadIdx.x >> 6) * (S * kFastJ * L * bpw);
-    constexpr int blocks_per_wg = kThreads >> lpb_log2;
+    // this lane's row (s, j) starts at dwave + ((s*J + j)*bpw + bw) * ROW; table words hold byte offsets into it
+    DT* dwave = reinterpret_cast<DT*>(smem + S * per) + (threadIdx.x >> 6) * (S * kFastJ * bpw * ROW);
+    const char* drow0 = reinterpret_cast<const char*>(dwave + bw * ROW);
     const int64_t ntiles = (nb + blocks_per_wg - 1) / blocks_per_wg;
     const float tiny = T::dt == kF16 ? 6.103515625e-05f : 1.17549435e-38f;
 
     for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-        const int64_t gb = tile * blocks_per_wg + (threadIdx.x >> lpb_log2);
+        const int64_t gb = tile * blocks_per_wg + (threadIdx.x / lpb);
         const bool valid = gb < nb;
         const int64_t off = (valid ? gb : 0) * (int64_t)block + (int64_t)li * kV;
 
-        float xv[kV];
-        if (valid) load16<T>(x + off, xv);
-        else {
+        // load 16 elements; the block max of |x| over the raw 16-bit patterns
+        uint32_t w[8];
+        if (valid) {
+            typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+            const u32x4_t* q = reinterpret_cast<const u32x4_t*>(x + off);
+            const u32x4_t a = __builtin_nontemporal_load(q), b = __builtin_nontemporal_load(q + 1);
+            w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+        } else {
 #pragma unroll
-            for (int i = 0; i < kV; ++i) xv[i] = 0.f;
+            for (int i = 0; i < 8; ++i) w[i] = 0u;
         }
-        uint32_t mb = 0;
-        float xa[kV];
+        uint32_t m2 = 0;
 #pragma unroll
-        for (int i = 0; i < kV; ++i) {
-            xa[i] = fabsf(xv[i]);
-            const uint32_t b = f2bits(xa[i]);
-            mb = mb > b ? mb : b;
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t a = w[i] & 0x7fff7fffu;
+            const uint32_t lo = a & 0xffffu, hi = a >> 16;
+            const uint32_t mx = lo > hi ? lo : hi;
+            m2 = m2 > mx ? m2 : mx;
         }
-        const float amax = bits2f(group_max_bits(mb, lpb));
+        m2 = max8_dpp(m2);
+        const float amax = T::load((typename T::storage)m2);
+        float xv[kV], xa[kV];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            xv[2 * i] = T::load((typename T::storage)(w[i] & 0xffffu));
+            xv[2 * i + 1] = T::load((typename T::storage)(w[i] >> 16));
+            xa[2 * i] = fabsf(xv[2 * i]);
+            xa[2 * i + 1] = fabsf(xv[2 * i + 1]);
+        }
 
         float l1[S];
 #pragma unroll
-        for (int s = 0; s < S; ++s) l1[s] = scale_quant<T>(T::round(amax / p.em[s]), p.sf);
+        for (int s = 0; s < S; ++s) {
+            float sc = T::round(amax / p.em[s]);
+            sc = sc < 6.103515625e-05f ? 6.103515625e-05f : (sc > 61440.f ? 61440.f : sc);
+            l1[s] = sc != sc ? sc : e5m3_scale<T>(sc, p.use_ceil);
+        }
 
         // magnitudes R_T(R_T(level * l2_j) * l1_s) of this block
-        for (int c = li; c < L; c += lpb) {
-            const int ef = c >> M, mf = c & ((1 << M) - 1);
-            const float v = ef == 0 ? (float)mf * (1.0f / (float)(1 << M))
-                                    : (1.0f + (float)mf * (1.0f / (float)(1 << M))) * pow2f(ef - 1);
 #pragma unroll
-            for (int s = 0; s < S; ++s)
+        for (int s = 0; s < S; ++s)
 #pragma unroll
-                for (int j = 0; j < kFastJ; ++j)
-                    dtab[dtab_index<S, L>(s, j, c, bw, bpw)] = (DTabT<T>)T::round(T::round(v * l2v[s][j]) * l1[s]);
-        }
+            for (int j = 0; j < kFastJ; ++j)
+#pragma unroll
+                for (int k = 0; k < CPL; ++k) {
+                    const int c = li + k * lpb;
+                    if (c < L) dwave[((s * kFastJ + j) * bpw + bw) * ROW + c] = (DT)T::round(qs[s][j][k] * l1[s]);
+                }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -205,7 +253,7 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
         h2_t xp[kV / 2];
         if constexpr (T::dt == kF16) {
 #pragma unroll
-            for (int i = 0; i < kV; i += 2) xp[i / 2] = (h2_t){(_Float16)xa[i], (_Float16)xa[i + 1]};
+            for (int i = 0; i < 8; ++i) xp[i] = __builtin_bit_cast(h2_t, w[i] & 0x7fff7fffu);
         }
         uint32_t ent[S][kV];
         float tq[S][kV];
@@ -235,27 +283,24 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
 #pragma unroll
             for (int j = 0; j < kFastJ; ++j) {
                 if (j >= p.J) break;
+                const char* rowb = drow0 + ((s * kFastJ + j) * bpw) * ROW * sizeof(DT);
 #pragma unroll
                 for (int sb = 0; sb < NSUBL; ++sb) {
                     float acc = 0.f;
 #pragma unroll
                     for (int i = sb * SUBN; i < (sb + 1) * SUBN; i += 2) {
-                        const int lv0 = (int)((ent[s][i] >> (8 * j)) & 0xffu);
-                        const int lv1 = (int)((ent[s][i + 1] >> (8 * j)) & 0xffu);
+                        const DT d0 = *reinterpret_cast<const DT*>(rowb + ((ent[s][i] >> (8 * j)) & 0xffu));
+                        const DT d1 = *reinterpret_cast<const DT*>(rowb + ((ent[s][i + 1] >> (8 * j)) & 0xffu));
                         if constexpr (T::dt == kF16) {
                             // R16(|x| - d) and R16(e^2) are single correctly rounded fp16 ops
-                            const h2_t dp = {dtab[dtab_index<S, L>(s, j, lv0, bw, bpw)],
-                                             dtab[dtab_index<S, L>(s, j, lv1, bw, bpw)]};
-                            const h2_t e = xp[i / 2] - dp;
+                            const h2_t e = xp[i / 2] - (h2_t){d0, d1};
                             h2_t q = e * e;
                             asm("" : "+v"(q));
                             acc += (float)q.x;
                             acc += (float)q.y;
                         } else {
-                            const float d0 = dtab[dtab_index<S, L>(s, j, lv0, bw, bpw)];
-                            const float d1 = dtab[dtab_index<S, L>(s, j, lv1, bw, bpw)];
                             float e0, e1, q0, q1;
-                            round2<T>(xa[i] - d0, xa[i + 1] - d1, e0, e1);
+                            round2<T>(xa[i] - (float)d0, xa[i + 1] - (float)d1, e0, e1);
                             round2<T>(e0 * e0, e1 * e1, q0, q1);
                             acc += q0;
                             acc += q1;
@@ -284,9 +329,10 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
 #pragma unroll
             for (int i = 0; i < kV; ++i) {
                 const int j = jsel[s][i / SUBN];
-                const uint32_t lev = (ent[s][i] >> (8 * j)) & 0xffu;
-                lsel[s][i] = lev;
-                msel[s][i] = (float)dtab[dtab_index<S, L>(s, j, (int)lev, bw, bpw)];
+                const uint32_t off8 = (ent[s][i] >> (8 * j)) & 0xffu;
+                lsel[s][i] = off8 / sizeof(DT);
+                const char* a = drow0 + ((s * kFastJ + j) * bpw) * ROW * sizeof(DT) + off8;
+                msel[s][i] = (float)*reinterpret_cast<const DT*>(a);
             }
         int sstar = 0;
         if constexpr (S == 2) {
@@ -338,12 +384,12 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
                     }
                     *reinterpret_cast<uint2*>(codes + off / 2) = make_uint2(w0, w1);
                 } else {
-                    uint32_t w[4];
+                    uint32_t cw[4];
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        w[i] = (cout[4 * i] & 0xffu) | ((cout[4 * i + 1] & 0xffu) << 8) |
-                               ((cout[4 * i + 2] & 0xffu) << 16) | ((cout[4 * i + 3] & 0xffu) << 24);
-                    *reinterpret_cast<uint4*>(codes + off) = make_uint4(w[0], w[1], w[2], w[3]);
+                        cw[i] = (cout[4 * i] & 0xffu) | ((cout[4 * i + 1] & 0xffu) << 8) |
+                                ((cout[4 * i + 2] & 0xffu) << 16) | ((cout[4 * i + 3] & 0xffu) << 24);
+                    *reinterpret_cast<uint4*>(codes + off) = make_uint4(cw[0], cw[1], cw[2], cw[3]);
                 }
             }
             if (li == 0) {
@@ -351,7 +397,7 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
                 if (sch_out) sch_out[gb] = (uint8_t)sstar;
             }
             if (l2i_out) {
-                const int nsub_blk = block / L2B;
+                constexpr int nsub_blk = block / L2B;
                 const int s = (S == 2 && sstar) ? S - 1 : 0;
                 if (L2B <= kV) {
 #pragma unroll
@@ -399,15 +445,15 @@ int build_slot(int slot, const FastParams& p, hipStream_t st) {
     return status;   // 0 ready, > 0 the table shape does not fit this configuration
 }
 
-template <class T, int M, int L2B, int S, int LPB_LOG2>
-int launch_fast_b(const void* x, void* y, void* l1, void* l2i, void* sch, void* codes, int64_t nb, int slot,
-                  const FastParams& p, int dev, hipStream_t st) {
-    constexpr int lpb_log2 = LPB_LOG2;
+template <class T, int M, int L2B, int S>
+int launch_fast(const void* x, void* y, void* l1, void* l2i, void* sch, void* codes, int64_t nb, int slot,
+                const FastParams& p, int dev, hipStream_t st) {
+    constexpr int lpb_log2 = 3;
     using St = typename T::storage;
     const size_t lds = (size_t)S * (p.n + 2) * 4 +
-                       (size_t)(kThreads >> lpb_log2) * S * kFastJ * (1 << (M + 2)) * sizeof(DTabT<T>);
+                       (size_t)(kThreads >> lpb_log2) * S * kFastJ * ((1 << (M + 2)) + 1) * sizeof(DTabT<T>);
     if (lds > 160 * 1024) return 0;
-    auto kern = hbq_fast_kernel<T, M, L2B, S, LPB_LOG2>;
+    auto kern = hbq_fast_kernel<T, M, L2B, S>;
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kThreads, lds) != hipSuccess || per_cu <= 0)
         return 0;
@@ -420,22 +466,12 @@ int launch_fast_b(const void* x, void* y, void* l1, void* l2i, void* sch, void* 
     return 1;
 }
 
-template <class T, int M, int L2B, int S>
-int launch_fast(const void* x, void* y, void* l1, void* l2i, void* sch, void* codes, int64_t cols, int block,
-                int lpb_log2, int64_t nb, int slot, const FastParams& p, int dev, hipStream_t st) {
-    (void)cols;
-    (void)block;
-    // block 128 (the HBQ configurations); other block sizes take the generic kernel
-    if (lpb_log2 == 3) return launch_fast_b<T, M, L2B, S, 3>(x, y, l1, l2i, sch, codes, nb, slot, p, dev, st);
-    return 0;
-}
-
 template <class T, int M>
 int fast_by_shape(int l2b, int S, const void* x, void* y, void* l1, void* l2i, void* sch, void* codes, int64_t cols,
                   int block, int lpb_log2, int64_t nb, int slot, const FastParams& p, int dev, hipStream_t st) {
 #define FAST_CASE(LB, SS)                                                                                   \
     if (l2b == LB && S == SS)                                                                               \
-        return launch_fast<T, M, LB, SS>(x, y, l1, l2i, sch, codes, cols, block, lpb_log2, nb, slot, p, dev, st);
+        return launch_fast<T, M, LB, SS>(x, y, l1, l2i, sch, codes, nb, slot, p, dev, st);
     FAST_CASE(8, 1) FAST_CASE(8, 2) FAST_CASE(16, 1) FAST_CASE(16, 2) FAST_CASE(32, 1) FAST_CASE(32, 2)
 #undef FAST_CASE
     return 0;
@@ -479,7 +515,9 @@ int hbq_fast_try(const void* x, void* y, void* l1, void* l2i, void* sch, void* c
         for (int s = 0; s < 2; ++s) p.l2[j][s] = j < hp.J ? hp.l2[j][s] : 1.f;
     p.em[0] = hp.em[0];
     p.em[1] = hp.em[S - 1];
-    p.sf = hp.sf;
+    p.use_ceil = hp.sf.use_ceil;
+    // the kernel quantizes the L1 scale to E5M3 without subnormals
+    if (hp.sf.allow_sub || hp.sf.emax != 15.f || hp.sf.mshift != 8.f || hp.sf.emin != -14.f) return 0;
 
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;

@@ -139,6 +139,21 @@ __device__ __forceinline__ float scale_quant(float s, const ScaleFmt& f) {
     return q;
 }
 
+// E5M3 scale quantization of a positive normal T value s in [2^-14, 61440]
+// (the L1 scale after its clip): rounding the fp32 mantissa to 3 bits half-up
+// (or up, with use_ceil) is the reference's floor(R_T(|m| + 0.5)) / ceil(|m|)
+// with the carry into the next binade.  With ceil, values whose R_T-rounded
+// log2 already reaches the next binade take 1.125 * 2^(e+1) as in the reference.
+template <class T>
+__device__ __forceinline__ float e5m3_scale(float s, int use_ceil) {
+    const uint32_t b = f2bits(s);
+    if (!use_ceil) return bits2f((b + 0x80000u) & 0xfff00000u);
+    const float q = bits2f((b + 0xfffffu) & 0xfff00000u);
+    const int e = binade(s);
+    const bool quirk = log2_exponent<T>(s, 0) > (float)e;
+    return quirk ? 1.125f * pow2f(e + 1) : q;
+}
+
 // ---- element quantizer for E2Mm (src/quantizer.py:202-255, allow_subnormal=True).
 // u is a T value.  Returns the quantized element value (in T) and its code
 // [sign | exponent field (2 bits) | mantissa (m bits)], exponent field 0 for
