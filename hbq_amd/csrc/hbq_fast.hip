@@ -256,26 +256,33 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
             for (int i = 0; i < 8; ++i) xp[i] = __builtin_bit_cast(h2_t, w[i] & 0x7fff7fffu);
         }
         uint32_t ent[S][kV];
-        float tq[S][kV];
+        uint32_t tb[S][kV];      // bit patterns of t = R_T(|x| / l1): non-negative, so ordered as integers
         int jsel[S][NSUBL];
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             const float rl1 = 1.0f / l1[s];
-            bool exact = false;
+            float qmin = xa[0] * rl1;
 #pragma unroll
             for (int i = 0; i < kV; i += 2) {
                 const float q0 = xa[i] * rl1, q1 = xa[i + 1] * rl1;
-                exact |= (q0 < tiny) | (q1 < tiny);
-                round2<T>(q0, q1, tq[s][i], tq[s][i + 1]);
+                qmin = fminf(qmin, fminf(q0, q1));
+                if constexpr (T::dt == kBF16) {
+                    const uint32_t r = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){q0, q1}, bf16x2_t));
+                    tb[s][i] = r & 0xffffu;
+                    tb[s][i + 1] = r >> 16;
+                } else {
+                    tb[s][i] = bits_of<T>(T::round(q0));
+                    tb[s][i + 1] = bits_of<T>(T::round(q1));
+                }
             }
-            if (exact) {   // quotients in T's subnormal range can be exact ties: divide
+            if (qmin < tiny) {   // quotients in T's subnormal range can be exact ties: divide
 #pragma unroll
                 for (int i = 0; i < kV; ++i)
-                    if (xa[i] * rl1 < tiny) tq[s][i] = T::round(xa[i] / l1[s]);
+                    if (xa[i] * rl1 < tiny) tb[s][i] = bits_of<T>(T::round(xa[i] / l1[s]));
             }
 #pragma unroll
             for (int i = 0; i < kV; ++i) {
-                int k = (int)bits_of<T>(tq[s][i]) - (int)p.lo_bits + 1;
+                int k = (int)tb[s][i] - (int)p.lo_bits + 1;
                 k = k < 0 ? 0 : (k > p.n + 1 ? p.n + 1 : k);
                 ent[s][i] = lut[s * per + k];
             }
@@ -352,7 +359,7 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
 
         float out[kV];
         uint32_t cout[kV];
-        float zsel[NSUBL];
+        uint32_t zsel[NSUBL];
 #pragma unroll
         for (int sb = 0; sb < NSUBL; ++sb) {
             const int s = (S == 2 && sstar) ? S - 1 : 0;
@@ -360,12 +367,12 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
             float zz = z[s][0];
 #pragma unroll
             for (int jj = 1; jj < kFastJ; ++jj) zz = j == jj ? z[s][jj] : zz;
-            zsel[sb] = zz;
+            zsel[sb] = bits_of<T>(zz);
         }
 #pragma unroll
         for (int i = 0; i < kV; ++i) {
             const bool s1 = S == 2 && sstar;
-            const float t = s1 ? tq[S - 1][i] : tq[0][i];
+            const uint32_t t = s1 ? tb[S - 1][i] : tb[0][i];
             const bool neg = (f2bits(xv[i]) >> 31) && t >= zsel[i / SUBN];
             const float m = s1 ? msel[S - 1][i] : msel[0][i];
             out[i] = neg ? -m : m;
