@@ -135,12 +135,13 @@ def mx_launcher(x, cfg, codes=True):
 
 
 GEMM_CASES = [
-    # (name, M, K, N, op, group_k, group_n, weight layout)
-    ("cfg2_gateup_mxint8_kn", 4096, 4096, 14336, "mxint8", 128, 32, "kn"),
+    # (name, M, K, N, op, group_k, group_n, B layout): "nk" = W[N, K] as FP16AccumMatMul passes it,
+    # "kn" = B[K, N] as the blockquant_ext ops take it
     ("cfg2_gateup_mxint8_nk", 4096, 4096, 14336, "mxint8", 128, 32, "nk"),
-    ("cfg2_gateup_grouped_kn", 4096, 4096, 14336, "grouped", 128, 0, "kn"),
-    ("cfg2_down_grouped_kn", 4096, 14336, 4096, "grouped", 128, 0, "kn"),
-    ("cfg3_mxint8_kn", 8192, 4096, 4096, "mxint8", 128, 32, "kn"),
+    ("cfg2_gateup_mxint8_kn", 4096, 4096, 14336, "mxint8", 128, 32, "kn"),
+    ("cfg2_gateup_grouped_nk", 4096, 4096, 14336, "grouped", 128, 0, "nk"),
+    ("cfg2_down_grouped_nk", 4096, 14336, 4096, "grouped", 128, 0, "nk"),
+    ("cfg3_mxint8_nk", 8192, 4096, 4096, "mxint8", 128, 32, "nk"),
 ]
 
 
@@ -159,7 +160,7 @@ def gemm_extra(dev, cases=GEMM_CASES, iters=10):
             fn = lambda: ext.gemm_blockquant_mxint8(A, B, gk, gn, b_is_nk=nk)
         else:
             fn = lambda: ext.gemm_fp16_grouped_accum(A, B, gk, b_is_nk=nk)
-        for _ in range(2):
+        for _ in range(5 if name == cases[0][0] else 2):   # the first case also brings the clocks up
             fn()
         t = HipTimer().run(fn, iters)
         tf = 2.0 * M * N * K / t / 1e12

@@ -34,14 +34,24 @@ def _check_inputs(A, B, b_is_nk=False):
         raise RuntimeError("A's K dimension must match B's K dimension")
 
 
-def _prep(A, B, b_is_nk):
+# B[K, N] operands of at least this many multiply-adds are transposed to W[N, K]
+# first: the 256x256-tile kernel reads W[N, K] (K contiguous), and the copy costs
+# a few percent of such a GEMM.  Both layouts give bit-identical results (the
+# same MFMA sequence per output element).
+TRANSPOSE_MIN_MNK = 1 << 30
+
+
+def _prep(A, B, b_is_nk, group_k=64):
     _check_inputs(A, B, b_is_nk)
     A = A.contiguous()
-    B = B.contiguous()
     M, K = A.shape
     N = B.size(0) if b_is_nk else B.size(1)
+    if not b_is_nk and M * N * K >= TRANSPOSE_MIN_MNK and K % 64 == 0 and N % 8 == 0 and group_k >= 64:
+        B, b_is_nk = B.t().contiguous(), True
+    else:
+        B = B.contiguous()
     C = torch.empty((M, N), dtype=torch.float16, device=A.device)
-    return A, B, C, M, N, K
+    return A, B, C, M, N, K, b_is_nk
 
 
 def _call(fn, *args):
@@ -50,7 +60,7 @@ def _call(fn, *args):
 
 def gemm_fp32_accum(A, B, b_is_nk=False):
     """fp32 accumulation over all of K, one rounding to fp16 (gemm.cu:593-616)."""
-    A, B, C, M, N, K = _prep(A, B, b_is_nk)
+    A, B, C, M, N, K, b_is_nk = _prep(A, B, b_is_nk)
     _call(_lib.lib().hbq_gemm_fp32_accum, _lib.ptr(A), _lib.ptr(B), _lib.ptr(C), M, N, K, int(b_is_nk),
           _lib.stream_of(A))
     return C
@@ -58,7 +68,7 @@ def gemm_fp32_accum(A, B, b_is_nk=False):
 
 def gemm_fp16_accum(A, B, b_is_nk=False):
     """fp16 fused multiply-add chain over ascending k (gemm.cu:568-591)."""
-    A, B, C, M, N, K = _prep(A, B, b_is_nk)
+    A, B, C, M, N, K, b_is_nk = _prep(A, B, b_is_nk, group_k=0)
     _call(_lib.lib().hbq_gemm_fp16_accum, _lib.ptr(A), _lib.ptr(B), _lib.ptr(C), M, N, K, int(b_is_nk),
           _lib.stream_of(A))
     return C
@@ -66,7 +76,7 @@ def gemm_fp16_accum(A, B, b_is_nk=False):
 
 def gemm_fp16_grouped_accum(A, B, group_k, b_is_nk=False):
     """fp32 within each group_k-wide K group, fp16 accumulation across groups (gemm.cu:618-667)."""
-    A, B, C, M, N, K = _prep(A, B, b_is_nk)
+    A, B, C, M, N, K, b_is_nk = _prep(A, B, b_is_nk, group_k)
     _call(_lib.lib().hbq_gemm_fp16_grouped_accum, _lib.ptr(A), _lib.ptr(B), _lib.ptr(C), M, N, K, int(group_k),
           int(b_is_nk), _lib.stream_of(A))
     return C
@@ -74,7 +84,7 @@ def gemm_fp16_grouped_accum(A, B, group_k, b_is_nk=False):
 
 def gemm_blockquant_mxfp8(A, B, group_k, group_n, b_is_nk=False):
     """Per-K-group partials quantized to E3M4 per (row, group_n columns), fp16 accumulation (gemm.cu:1040-1135)."""
-    A, B, C, M, N, K = _prep(A, B, b_is_nk)
+    A, B, C, M, N, K, b_is_nk = _prep(A, B, b_is_nk, group_k)
     _call(_lib.lib().hbq_gemm_blockquant_mxfp8, _lib.ptr(A), _lib.ptr(B), _lib.ptr(C), M, N, K, int(group_k),
           int(group_n), int(b_is_nk), _lib.stream_of(A))
     return C
@@ -83,7 +93,7 @@ def gemm_blockquant_mxfp8(A, B, group_k, group_n, b_is_nk=False):
 def gemm_blockquant_mxint8(A, B, group_k, group_n, b_is_nk=False):
     """Per-K-group partials quantized to INT8 with a power-of-two scale per (row, group_n columns),
     fp16 accumulation across groups (gemm.cu:1399-1478)."""
-    A, B, C, M, N, K = _prep(A, B, b_is_nk)
+    A, B, C, M, N, K, b_is_nk = _prep(A, B, b_is_nk, group_k)
     _call(_lib.lib().hbq_gemm_blockquant_mxint8, _lib.ptr(A), _lib.ptr(B), _lib.ptr(C), M, N, K, int(group_k),
           int(group_n), int(b_is_nk), _lib.stream_of(A))
     return C

@@ -1,128 +1,36 @@
-// Block-quant GEMMs of blockquant_ext on gfx950 MFMA.
+// Block-quant GEMMs of blockquant_ext on gfx950 MFMA: the C-ABI entry points,
+// the 128x128-tile kernel and the pure-fp16 FMA-chain kernel.
 //
 // C[M,N] (fp16) = A[M,K] (fp16) x B[K,N] (fp16), with B either row-major
 // [K,N] as the reference op takes it, or stored transposed as W[N,K] (the
 // nn.Linear weight layout, which skips the caller's transpose copy).
 //
-// The K dimension is cut into groups of GK.  Inside a group the fp32 partial
-// comes from v_mfma_f32_32x32x16_f16; at the end of each group an epilogue
-// fused into the kernel folds the partial into an fp16 accumulator exactly as
-// the reference does after its sequential fmaf chain
-// (blockquant_ext_src/gemm.cu:354-377, 810-887, 1198-1277):
-//   grouped : H = R16(H + R16(P))
-//   mxint8  : per (row, GN columns) s = 2^(ilogb(max|P|) - 6), Q = clamp(rne(P/s), +-127) * s,
-//             H = R16(H + R16(Q))
-//   mxfp8   : same with E3M4 quantize-dequantize and s = 2^(ilogb(max|P|) - 3)
-//   fp32    : one group spanning K, C = R16(P)
-//   partial : P of every group written out (fp32), for checking the epilogue
+// The K dimension is cut into groups of group_k.  Inside a group the fp32
+// partial comes from v_mfma_f32_32x32x16_f16; at the end of each group the
+// epilogue of gemm_common.h folds it into the fp16 accumulators as the
+// reference does after its sequential fmaf chain; fp32 accumulation is one
+// group spanning K, and the partial mode writes every group's fp32 partial.
 //
-// Operand order is swapped (D = B^T A^T): the MFMA "row" is the output column
-// n and the MFMA "column" is the output row m, so lane l owns row m = l % 32
-// of a 32x32 block and 16 of its 32 columns (n = 8*(r/4) + 4*(l/32) + r%4);
-// the other 16 sit in lane l ^ 32.  A psum group of up to 32 columns of one
-// row therefore needs one cross-lane exchange.
+// W[N,K] operands with K % 64 == 0 and group_k >= 64 go to the 256x256-tile
+// kernel (gemm_tile256.hip); everything else runs here: 128x128 tiles, 4
+// waves of 64x64, register-staged LDS double buffering, B[K,N] transposed into
+// LDS by 16-bit scatters.  Both kernels issue the same MFMA sequence per
+// output element, so they give the same bits.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
 
+#include "gemm_common.h"
+#include "gemm_tile256.h"
 #include "hbq_capi_internal.h"
 
 namespace hbq_gemm {
-
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef float f16v __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-enum Mode : int { kGrouped = 0, kInt8 = 1, kFp8 = 2, kFp32 = 3, kPartial = 4 };
 
 constexpr int BM = 128;          // output rows per workgroup
 constexpr int BN = 128;          // output columns per workgroup
 constexpr int BK = 64;           // K per LDS stage
 constexpr int LDK = BK + 8;      // padded LDS row (halfs): 144 B, conflict-free 16 B reads
 constexpr int kThreads = 256;
-
-__device__ __forceinline__ float f16r(float v) {
-    _Float16 h = (_Float16)v;
-    asm("" : "+v"(h));
-    return (float)h;
-}
-
-// ---- psum quantizers (gemm.cu:677-745, 1145-1251) --------------------------
-__device__ __forceinline__ float int8_qdq(float p, float s, float inv) {
-    float v = p * inv;
-    if (v != v) return v;
-    float q = rintf(v);
-    q = q > 127.f ? 127.f : (q < -127.f ? -127.f : q);
-    return q * s;
-}
-
-__device__ __forceinline__ float e3m4_qdq(float x, float scale) {
-    float sgn = copysignf(1.f, x);
-    float a = fabsf(x);
-    if (a == 0.f) return copysignf(0.f, x);
-    float y = a / scale;
-    if (!isfinite(y)) {
-        if (isnan(y)) return copysignf(__builtin_nanf(""), x);
-        return sgn * 15.5f * scale;
-    }
-    if (y < 0.5f * 0.015625f) return 0.f;
-    if (y >= 0.25f) {
-        int e = __builtin_amdgcn_frexp_expf(y) - 1;   // exact floor(log2 y)
-        e = e < -2 ? -2 : (e > 3 ? 3 : e);
-        float p2 = __builtin_amdgcn_ldexpf(1.f, e);
-        float frac = y / p2 - 1.f;
-        float mant = rintf(frac * 16.f);
-        if (mant >= 16.f) {
-            mant = 0.f;
-            ++e;
-            if (e > 3) { e = 3; mant = 15.f; }
-            p2 = __builtin_amdgcn_ldexpf(1.f, e);
-        }
-        float yq = (1.f + mant * (1.f / 16.f)) * p2;
-        if (yq > 15.5f) yq = 15.5f;
-        return sgn * yq * scale;
-    }
-    float mant = rintf(y * 64.f);
-    if (mant <= 0.f) return 0.f;
-    if (mant >= 16.f) return sgn * 0.25f * scale;
-    float yq = (mant * (1.f / 16.f)) * 0.25f;
-    return sgn * yq * scale;
-}
-
-// power-of-two psum scale 2^(ilogb(mx) - shift); 1 for an all-zero group; inf for an inf max
-__device__ __forceinline__ float psum_scale(float mx, int shift) {
-    if (!(mx > 0.f)) return 1.f;
-    if (mx == __builtin_inff()) return __builtin_inff();
-    return __builtin_amdgcn_ldexpf(1.f, __builtin_amdgcn_frexp_expf(mx) - 1 - shift);
-}
-
-// Fold the 16 fp32 partials of one 32x32 block into the fp16 accumulators.
-template <int MODE, int GN>
-__device__ __forceinline__ void fold_block(f16v& acc, float* H) {
-    if constexpr (MODE == kGrouped) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) H[r] = f16r(H[r] + f16r(acc[r]));
-    } else {
-        // registers of one column group: GN=4 -> r/4 within a lane-half pair, else r/(GN/2) across l^32
-        constexpr int RPG = GN >= 8 ? GN / 2 : 4;     // registers per group in this lane
-        constexpr int NG = 16 / RPG;
-        constexpr int shift = MODE == kInt8 ? 6 : 3;
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-            float mx = 0.f;
-#pragma unroll
-            for (int r = g * RPG; r < (g + 1) * RPG; ++r) mx = fmaxf(mx, fabsf(acc[r]));
-            if constexpr (GN >= 8) mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float s = psum_scale(mx, shift);
-            const float inv = 1.f / s;
-#pragma unroll
-            for (int r = g * RPG; r < (g + 1) * RPG; ++r) {
-                float q = MODE == kInt8 ? int8_qdq(acc[r], s, inv) : e3m4_qdq(acc[r], s);
-                H[r] = f16r(H[r] + f16r(q));
-            }
-        }
-    }
-}
 
 // ---- global -> LDS tile loads ----------------------------------------------
 // A tile: rows m0..m0+BM, k0..k0+BK, k contiguous.  Chunk c (8 halfs): row c / 8, col (c % 8) * 8.
@@ -141,11 +49,12 @@ __device__ __forceinline__ u32x4 load_chunk(const uint16_t* __restrict__ base, i
 }
 
 // ---- the kernel ------------------------------------------------------------
-template <int MODE, int GK, int GN, bool BT>
+// SMALLG: group_k < BK (16 or 32), so group ends fall inside an LDS stage.
+template <int MODE, int GN, bool BT, bool SMALLG>
 __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const uint16_t* __restrict__ A,
                                                             const uint16_t* __restrict__ B,
                                                             uint16_t* __restrict__ C, float* __restrict__ P, int M,
-                                                            int N, int K, int vec_a, int vec_b) {
+                                                            int N, int K, int gk, int vec_a, int vec_b) {
     __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][LDK];
     __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN][LDK];   // stored transposed: [n][k]
 
@@ -159,14 +68,14 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const uint16_t* __res
     const int nkt = (K + BK - 1) / BK;
 
     f16v acc[2][2];     // [n block][m block]
-    float H[2][2][16];
+    h2_t H[2][2][8];    // fp16 accumulators, packed pairs of adjacent columns
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             acc[i][j] = (f16v){};
 #pragma unroll
-            for (int r = 0; r < 16; ++r) H[i][j][r] = 0.f;
+            for (int p = 0; p < 8; ++p) H[i][j][p] = (h2_t){(_Float16)0.f, (_Float16)0.f};
         }
 
     // global tile loaders into registers
@@ -221,8 +130,35 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const uint16_t* __res
     swrite(0);
     __syncthreads();
 
-    int ks_global = 0;   // index of the next 16-wide k step
+    int ks_global = 0;   // k steps (16 wide) done
     const int nks = (K + 15) / 16;
+    const int gsteps = gk / 16;
+    // fold (or dump) the group partials and restart them
+    auto group_end = [&]() {
+        if constexpr (MODE == kPartial) {
+            const int g = (ks_global * 16 - 1) / gk;
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int64_t m = m0 + wm + j * 32 + (lane & 31);
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int64_t n = n0 + wn + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r & 3);
+                        if (m < M && n < N) P[((int64_t)g * M + m) * N + n] = acc[i][j][r];
+                    }
+                }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) fold_block<MODE, GN>(acc[i][j], H[i][j]);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[i][j] = (f16v){};
+    };
     for (int kt = 0; kt < nkt; ++kt) {
         const int buf = kt & 1;
         if (kt + 1 < nkt) gload(kt + 1);
@@ -242,35 +178,12 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const uint16_t* __res
                 for (int j = 0; j < 2; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bop[i], aop[j], acc[i][j], 0, 0, 0);
             ++ks_global;
-            if constexpr (MODE != kFp32) {
-                const bool group_end = ((ks_global * 16) % GK == 0) || (ks_global == nks);
-                if (group_end) {
-                    if constexpr (MODE == kPartial) {
-                        const int g = (ks_global * 16 - 1) / GK;
-#pragma unroll
-                        for (int i = 0; i < 2; ++i)
-#pragma unroll
-                            for (int j = 0; j < 2; ++j) {
-                                const int64_t m = m0 + wm + j * 32 + (lane & 31);
-#pragma unroll
-                                for (int r = 0; r < 16; ++r) {
-                                    const int64_t n = n0 + wn + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r & 3);
-                                    if (m < M && n < N) P[((int64_t)g * M + m) * N + n] = acc[i][j][r];
-                                }
-                            }
-                    } else {
-#pragma unroll
-                        for (int i = 0; i < 2; ++i)
-#pragma unroll
-                            for (int j = 0; j < 2; ++j) fold_block<MODE, GN>(acc[i][j], H[i][j]);
-                    }
-#pragma unroll
-                    for (int i = 0; i < 2; ++i)
-#pragma unroll
-                        for (int j = 0; j < 2; ++j) acc[i][j] = (f16v){};
-                }
-            }
+            if constexpr (SMALLG && MODE != kFp32)
+                if (ks_global % gsteps == 0 || ks_global == nks) group_end();
         }
+        // group_k >= BK: groups end on stage boundaries (or at the ragged end of K)
+        if constexpr (!SMALLG && MODE != kFp32)
+            if (ks_global % gsteps == 0 || ks_global == nks) group_end();
         if (kt + 1 < nkt) swrite(buf ^ 1);
         __syncthreads();
     }
@@ -286,18 +199,19 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const uint16_t* __res
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int64_t n = n0 + wn + i * 32 + 8 * q + 4 * (lane >> 5);
-                uint16_t h[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    float v = MODE == kFp32 ? acc[i][j][4 * q + e] : H[i][j][4 * q + e];
-                    _Float16 hv = (_Float16)v;
-                    asm("" : "+v"(hv));
-                    h[e] = __builtin_bit_cast(uint16_t, hv);
+                h2_t lo, hi;
+                if constexpr (MODE == kFp32) {
+                    lo = cvt2(acc[i][j][4 * q], acc[i][j][4 * q + 1]);
+                    hi = cvt2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+                } else {
+                    lo = H[i][j][2 * q];
+                    hi = H[i][j][2 * q + 1];
                 }
+                const uint32_t w0 = __builtin_bit_cast(uint32_t, lo), w1 = __builtin_bit_cast(uint32_t, hi);
+                const uint16_t h[4] = {(uint16_t)w0, (uint16_t)(w0 >> 16), (uint16_t)w1, (uint16_t)(w1 >> 16)};
                 uint16_t* dst = C + m * (int64_t)N + n;
                 if (n + 4 <= N && ((((uintptr_t)dst) & 7) == 0)) {
-                    *reinterpret_cast<uint2*>(dst) =
-                        make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+                    *reinterpret_cast<uint2*>(dst) = make_uint2(w0, w1);
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
@@ -362,34 +276,40 @@ using namespace hbq_gemm;
 
 namespace {
 
-template <int MODE, int GK, int GN, bool BT>
-void launch(const void* A, const void* B, void* C, float* P, int M, int N, int K, hipStream_t st) {
+template <int MODE, int GN, bool BT, bool SMALLG>
+void launch(const void* A, const void* B, void* C, float* P, int M, int N, int K, int gk, hipStream_t st) {
     dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
     int vec_a = (K % 8 == 0) && (((uintptr_t)A) % 16 == 0);
     int vec_b = (BT ? (K % 8 == 0) : (N % 8 == 0)) && (((uintptr_t)B) % 16 == 0);
-    hipLaunchKernelGGL((gemm_kernel<MODE, GK, GN, BT>), grid, dim3(kThreads), 0, st, (const uint16_t*)A,
-                       (const uint16_t*)B, (uint16_t*)C, P, M, N, K, vec_a, vec_b);
+    hipLaunchKernelGGL((gemm_kernel<MODE, GN, BT, SMALLG>), grid, dim3(kThreads), 0, st, (const uint16_t*)A,
+                       (const uint16_t*)B, (uint16_t*)C, P, M, N, K, gk, vec_a, vec_b);
 }
 
-template <int MODE, int GK, bool BT>
-int by_gn(int gn, const void* A, const void* B, void* C, int M, int N, int K, hipStream_t st) {
+// the 128x128 kernel for every case the 256x256 one does not take
+template <int MODE, int GN>
+void launch_any(const void* A, const void* B, void* C, float* P, int M, int N, int K, int gk, int b_is_nk,
+                hipStream_t st) {
+    if (launch_tile256(MODE, GN, A, B, C, P, M, N, K, gk, b_is_nk, st)) return;
+    const bool small = gk < BK;
+    if (b_is_nk) {
+        if (small) launch<MODE, GN, true, true>(A, B, C, P, M, N, K, gk, st);
+        else launch<MODE, GN, true, false>(A, B, C, P, M, N, K, gk, st);
+    } else {
+        if (small) launch<MODE, GN, false, true>(A, B, C, P, M, N, K, gk, st);
+        else launch<MODE, GN, false, false>(A, B, C, P, M, N, K, gk, st);
+    }
+}
+
+template <int MODE>
+int psum_dispatch(int gk, int gn, const void* A, const void* B, void* C, int M, int N, int K, int b_is_nk,
+                  hipStream_t st) {
     switch (gn) {
-        case 4: launch<MODE, GK, 4, BT>(A, B, C, nullptr, M, N, K, st); return 0;
-        case 8: launch<MODE, GK, 8, BT>(A, B, C, nullptr, M, N, K, st); return 0;
-        case 16: launch<MODE, GK, 16, BT>(A, B, C, nullptr, M, N, K, st); return 0;
-        case 32: launch<MODE, GK, 32, BT>(A, B, C, nullptr, M, N, K, st); return 0;
+        case 4: launch_any<MODE, 4>(A, B, C, nullptr, M, N, K, gk, b_is_nk, st); return 0;
+        case 8: launch_any<MODE, 8>(A, B, C, nullptr, M, N, K, gk, b_is_nk, st); return 0;
+        case 16: launch_any<MODE, 16>(A, B, C, nullptr, M, N, K, gk, b_is_nk, st); return 0;
+        case 32: launch_any<MODE, 32>(A, B, C, nullptr, M, N, K, gk, b_is_nk, st); return 0;
     }
     return hbq_fail(HBQ_ERR_INVALID, "group_n must be one of {4,8,16,32}");
-}
-
-template <int MODE, bool BT>
-int psum_dispatch(int gk, int gn, const void* A, const void* B, void* C, int M, int N, int K, hipStream_t st) {
-    switch (gk) {
-        case 64: return by_gn<MODE, 64, BT>(gn, A, B, C, M, N, K, st);
-        case 128: return by_gn<MODE, 128, BT>(gn, A, B, C, M, N, K, st);
-        case 256: return by_gn<MODE, 256, BT>(gn, A, B, C, M, N, K, st);
-    }
-    return hbq_fail(HBQ_ERR_INVALID, "group_k must be one of {64,128,256}");
 }
 
 int check_shapes(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K) {
@@ -426,8 +346,7 @@ int hbq_gemm_fp32_accum(const void* A, const void* B, void* C, int64_t M, int64_
     hipStream_t st = (hipStream_t)stream;
     if (M == 0 || N == 0) return 0;
     if (K == 0) return zero_output(C, M, N, st);
-    if (b_is_nk) launch<kFp32, 16, 4, true>(A, B, C, nullptr, (int)M, (int)N, (int)K, st);
-    else launch<kFp32, 16, 4, false>(A, B, C, nullptr, (int)M, (int)N, (int)K, st);
+    launch_any<kFp32, 4>(A, B, C, nullptr, (int)M, (int)N, (int)K, (int)K, b_is_nk, st);
     return hbq_check_launch("gemm_fp32_accum");
 }
 
@@ -453,13 +372,7 @@ int hbq_gemm_fp16_grouped_accum(const void* A, const void* B, void* C, int64_t M
     hipStream_t st = (hipStream_t)stream;
     if (M == 0 || N == 0) return 0;
     if (K == 0) return zero_output(C, M, N, st);
-#define GRP(G)                                                                                      \
-    case G:                                                                                         \
-        if (b_is_nk) launch<kGrouped, G, 4, true>(A, B, C, nullptr, (int)M, (int)N, (int)K, st);    \
-        else launch<kGrouped, G, 4, false>(A, B, C, nullptr, (int)M, (int)N, (int)K, st);           \
-        break;
-    switch (group_k) { GRP(16) GRP(32) GRP(64) GRP(128) }
-#undef GRP
+    launch_any<kGrouped, 4>(A, B, C, nullptr, (int)M, (int)N, (int)K, group_k, b_is_nk, st);
     return hbq_check_launch("gemm_fp16_grouped_accum");
 }
 
@@ -474,13 +387,8 @@ static int psum_common(int mode, const void* A, const void* B, void* C, int64_t 
     hipStream_t st = (hipStream_t)stream;
     if (M == 0 || N == 0) return 0;
     if (K == 0) return zero_output(C, M, N, st);
-    int rc;
-    if (mode == kInt8)
-        rc = b_is_nk ? psum_dispatch<kInt8, true>(gk, gn, A, B, C, (int)M, (int)N, (int)K, st)
-                     : psum_dispatch<kInt8, false>(gk, gn, A, B, C, (int)M, (int)N, (int)K, st);
-    else
-        rc = b_is_nk ? psum_dispatch<kFp8, true>(gk, gn, A, B, C, (int)M, (int)N, (int)K, st)
-                     : psum_dispatch<kFp8, false>(gk, gn, A, B, C, (int)M, (int)N, (int)K, st);
+    const int rc = mode == kInt8 ? psum_dispatch<kInt8>(gk, gn, A, B, C, (int)M, (int)N, (int)K, b_is_nk, st)
+                                 : psum_dispatch<kFp8>(gk, gn, A, B, C, (int)M, (int)N, (int)K, b_is_nk, st);
     if (rc) return rc;
     return hbq_check_launch(name);
 }
@@ -503,13 +411,7 @@ int hbq_gemm_group_partials(const void* A, const void* B, void* P, int64_t M, in
     if (int rc = check_shapes(A, B, P, M, N, K)) return rc;
     if (M == 0 || N == 0 || K == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
-#define GRP(G)                                                                                               \
-    case G:                                                                                                  \
-        if (b_is_nk) launch<kPartial, G, 4, true>(A, B, nullptr, (float*)P, (int)M, (int)N, (int)K, st);     \
-        else launch<kPartial, G, 4, false>(A, B, nullptr, (float*)P, (int)M, (int)N, (int)K, st);            \
-        break;
-    switch (group_k) { GRP(16) GRP(32) GRP(64) GRP(128) GRP(256) }
-#undef GRP
+    launch_any<kPartial, 4>(A, B, nullptr, (float*)P, (int)M, (int)N, (int)K, group_k, b_is_nk, st);
     return hbq_check_launch("gemm_group_partials");
 }
 

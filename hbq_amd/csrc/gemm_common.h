@@ -1,0 +1,191 @@
+// Shared pieces of the block-quant GEMM kernels: operand types, the psum
+// quantizers of blockquant_ext (blockquant_ext_src/gemm.cu:677-745, 1145-1251)
+// and the per-K-group epilogue that folds an fp32 MFMA partial into the fp16
+// accumulators (gemm.cu:354-377, 810-887, 1198-1277):
+//   grouped : H = R16(H + R16(P))
+//   mxint8  : per (row, GN columns) s = 2^(ilogb(max|P|) - 6), Q = clamp(rne(P/s), +-127) * s,
+//             H = R16(H + R16(Q))
+//   mxfp8   : same with E3M4 quantize-dequantize and s = 2^(ilogb(max|P|) - 3)
+//
+// Register layout (both kernels swap the MFMA operands, D = B^T A^T): a
+// v_mfma_f32_32x32x16_f16 accumulator of a 32x32 block holds, in lane l,
+// output row m = l % 32 and the 16 columns n = 8*(r/4) + 4*(l/32) + r%4 of
+// register r; the other 16 columns of that row sit in lane l ^ 32.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+namespace hbq_gemm {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef float f2_t __attribute__((ext_vector_type(2)));
+
+enum Mode : int { kGrouped = 0, kInt8 = 1, kFp8 = 2, kFp32 = 3, kPartial = 4 };
+
+// ---- psum quantizers -------------------------------------------------------
+__device__ __forceinline__ float int8_qdq(float p, float s, float inv) {
+    float v = p * inv;
+    if (v != v) return v;
+    float q = rintf(v);
+    q = q > 127.f ? 127.f : (q < -127.f ? -127.f : q);
+    return q * s;
+}
+
+__device__ __forceinline__ float e3m4_qdq(float x, float scale) {
+    float sgn = copysignf(1.f, x);
+    float a = fabsf(x);
+    if (a == 0.f) return copysignf(0.f, x);
+    float y = a / scale;
+    if (!isfinite(y)) {
+        if (isnan(y)) return copysignf(__builtin_nanf(""), x);
+        return sgn * 15.5f * scale;
+    }
+    if (y < 0.5f * 0.015625f) return 0.f;
+    if (y >= 0.25f) {
+        int e = __builtin_amdgcn_frexp_expf(y) - 1;   // exact floor(log2 y)
+        e = e < -2 ? -2 : (e > 3 ? 3 : e);
+        float p2 = __builtin_amdgcn_ldexpf(1.f, e);
+        float frac = y / p2 - 1.f;
+        float mant = rintf(frac * 16.f);
+        if (mant >= 16.f) {
+            mant = 0.f;
+            ++e;
+            if (e > 3) { e = 3; mant = 15.f; }
+            p2 = __builtin_amdgcn_ldexpf(1.f, e);
+        }
+        float yq = (1.f + mant * (1.f / 16.f)) * p2;
+        if (yq > 15.5f) yq = 15.5f;
+        return sgn * yq * scale;
+    }
+    float mant = rintf(y * 64.f);
+    if (mant <= 0.f) return 0.f;
+    if (mant >= 16.f) return sgn * 0.25f * scale;
+    float yq = (mant * (1.f / 16.f)) * 0.25f;
+    return sgn * yq * scale;
+}
+
+// power-of-two psum scale 2^(ilogb(mx) - shift); 1 for an all-zero group; inf for an inf max
+__device__ __forceinline__ float psum_scale(float mx, int shift) {
+    if (!(mx > 0.f)) return 1.f;
+    if (mx == __builtin_inff()) return __builtin_inff();
+    return __builtin_amdgcn_ldexpf(1.f, __builtin_amdgcn_frexp_expf(mx) - 1 - shift);
+}
+
+// R16 of two fp32 values in one v_cvt_pk_f16_f32 (round to nearest even)
+__device__ __forceinline__ h2_t cvt2(float a, float b) {
+    h2_t q = __builtin_convertvector((f2_t){a, b}, h2_t);
+    asm("" : "+v"(q));
+    return q;
+}
+
+// max with the partner lane l ^ 32.  v_permlane32_swap exchanges the upper
+// 32 lanes of its first operand with the lower 32 lanes of its second; with
+// both operands holding v, the two results together hold v of lane l ^ 32 in
+// every lane, whichever way the halves are assigned.  (Inline asm: the
+// compiler treats the two results of the builtin as equal when its operands
+// are, and drops one of them.)
+__device__ __forceinline__ float xlane32_max(float v) {
+    float a = v, b = v;
+    // s_nop: the VALU-write -> permlane-read hazard the compiler inserts for the builtin
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    return fmaxf(v, fmaxf(a, b));
+}
+
+// R16(t - M) written to the low or high half of h, in one v_fma_mix (t * 1 - M
+// with a single rounding of the exact difference)
+__device__ __forceinline__ void sub_to_lo(h2_t& h, float t, float M) {
+    asm("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,0]" : "+v"(h) : "v"(t), "v"(M));
+}
+__device__ __forceinline__ void sub_to_hi(h2_t& h, float t, float M) {
+    asm("v_fma_mixhi_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,0]" : "+v"(h) : "v"(t), "v"(M));
+}
+
+// Fold the 16 fp32 partials of one 32x32 block into the fp16 accumulators H
+// (8 packed pairs; pair p holds registers 2p and 2p + 1, adjacent columns).
+//
+// mxint8: for a group max mx that is finite and nonzero, s = 2^(e - 6) with
+// e = ilogb mx, |P| / s < 128, and rne(P / s) * s = (P + M) - M with
+// M = 1.5 * 2^(e + 17): the add rounds P to the nearest (even) multiple of
+// ulp(M) = s and the subtraction is exact.  (fp16 products bound |P| by 2^39
+// and nonzero |P| below by 2^-48, so M stays a normal fp32.)  NaN partials stay
+// NaN.  The subtraction and the rounding to fp16 share one v_fma_mix.
+// Only a group whose max lies in the top 1/128 of its binade can round to
+// +-128 s, which the clamp turns into +-127 s = +-128 s * 127/128; such
+// groups, all-zero groups (s = 1), groups with an infinite max (every output
+// NaN, as P / inf * inf) and maxima outside the normal range take a second,
+// rarely used branch.
+template <int MODE, int GN>
+__device__ __forceinline__ void fold_block(const f16v& acc, h2_t* H) {
+    if constexpr (MODE == kGrouped) {
+#pragma unroll
+        for (int p = 0; p < 8; ++p) H[p] = H[p] + cvt2(acc[2 * p], acc[2 * p + 1]);
+    } else {
+        constexpr int RPG = GN >= 8 ? GN / 2 : 4;     // registers of one column group in this lane
+        constexpr int NG = 16 / RPG;
+        float mxg[NG];
+        bool special = false;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            float mx = 0.f;
+#pragma unroll
+            for (int r = g * RPG; r < (g + 1) * RPG; ++r) mx = fmaxf(mx, fabsf(acc[r]));
+            if constexpr (GN >= 8) mx = xlane32_max(mx);
+            mxg[g] = mx;
+            const uint32_t mb = __builtin_bit_cast(uint32_t, mx);
+            special = special || (mb - 0x00800000u) >= (0x76000000u - 0x00800000u) || (mb & 0x7f0000u) == 0x7f0000u;
+        }
+        if constexpr (MODE == kInt8) {
+            if (!special) {
+#pragma unroll
+                for (int g = 0; g < NG; ++g) {
+                    const float M = __builtin_bit_cast(
+                        float, (__builtin_bit_cast(uint32_t, mxg[g]) & 0x7f800000u) + (17u << 23) + 0x400000u);
+#pragma unroll
+                    for (int r = g * RPG; r < (g + 1) * RPG; r += 2) {
+                        float t0 = acc[r] + M, t1 = acc[r + 1] + M;
+                        asm("" : "+v"(t0), "+v"(t1));
+                        h2_t q;
+                        sub_to_lo(q, t0, M);
+                        sub_to_hi(q, t1, M);
+                        H[r / 2] = H[r / 2] + q;
+                    }
+                }
+            } else {
+                float q[16];
+#pragma unroll
+                for (int g = 0; g < NG; ++g) {
+                    const float mx = mxg[g];
+                    const float s = psum_scale(mx, 6);
+                    const float M = s * 12582912.f;   // 1.5 * 2^23 * s
+                    const float c128 = 128.f * s;
+#pragma unroll
+                    for (int r = g * RPG; r < (g + 1) * RPG; ++r) {
+                        float t = acc[r] + M;
+                        asm("" : "+v"(t));
+                        t = t - M;
+                        t = fabsf(t) == c128 ? t * 0.9921875f : t;
+                        q[r] = mx == __builtin_inff() ? __builtin_nanf("") : t;
+                    }
+                }
+#pragma unroll
+                for (int p = 0; p < 8; ++p) H[p] = H[p] + cvt2(q[2 * p], q[2 * p + 1]);
+            }
+        } else {
+            float q[16];
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                const float s = psum_scale(mxg[g], 3);
+#pragma unroll
+                for (int r = g * RPG; r < (g + 1) * RPG; ++r) q[r] = e3m4_qdq(acc[r], s);
+            }
+#pragma unroll
+            for (int p = 0; p < 8; ++p) H[p] = H[p] + cvt2(q[2 * p], q[2 * p + 1]);
+        }
+    }
+}
+
+}  // namespace hbq_gemm

@@ -1,0 +1,13 @@
+// The 256x256-tile block-quant GEMM (gemm_tile256.hip): W[N,K] operand layout,
+// K a multiple of 64, N a multiple of 8, 16-byte aligned operands.
+#pragma once
+#include <hip/hip_runtime.h>
+
+namespace hbq_gemm {
+
+// Launches the 256x256 kernel for (mode, group_n) when the shape and layout
+// allow it and returns 1; returns 0 (nothing launched) otherwise.
+int launch_tile256(int mode, int gn, const void* A, const void* B, void* C, float* P, int M, int N, int K, int gk,
+                   int b_is_nk, hipStream_t st);
+
+}  // namespace hbq_gemm

@@ -1,0 +1,296 @@
+// 256x256-tile block-quant GEMM for gfx950, C[M,N] = A[M,K] W[N,K]^T (fp16).
+//
+// One 512-thread workgroup (8 waves) per 256x256 output tile; each wave owns
+// a 128 (rows) x 64 (columns) sub-tile: 4 x 2 blocks of
+// v_mfma_f32_32x32x16_f16 with the operands swapped (see gemm_common.h), so a
+// psum group of up to 32 columns of one row lives in one lane pair.
+//
+// Operand staging: 64-wide K slices of A and W go straight from global memory
+// into LDS with buffer_load_dwordx4 ... lds (no register staging), double
+// buffered (2 x 64 KB).  A row of a slice is 128 B = 8 chunks of 16 B, stored
+// in a swizzled order (swz_pos) that keeps the 16-byte operand reads of
+// consecutive rows free of bank conflicts.
+//
+// Tile order: consecutive workgroups go round-robin to the 8 XCDs, so tile
+// indices are first regrouped to give each XCD a contiguous range, then
+// walked in 4-row-tile column bands: the tiles resident on one XCD share A
+// rows and W rows in that XCD's L2.
+//
+// Group ends (group_k >= 64) fall on stage boundaries; group_k 16/32 (grouped
+// accumulation only) fold inside a stage.  At the end the fp16 accumulators go
+// through LDS to give full 128-byte row segments on the store.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "gemm_common.h"
+#include "gemm_tile256.h"
+
+namespace hbq_gemm {
+namespace t256 {
+
+constexpr int TM = 256, TN = 256, TK = 64, NT = 512;
+constexpr int SLICE = TM * TK;   // halfs of one operand slice (32 KB)
+
+// chunk c of row r sits at chunk position c ^ (r % 8) ^ ((r / 8) % 2): any 8
+// consecutive rows use 8 different positions, and any 16 consecutive rows 16
+// different (row parity, position) pairs, so 16-byte reads of consecutive rows
+// spread over all banks for a 128-byte as well as a 256-byte bank period
+__device__ __forceinline__ int swz_pos(int row, int chunk) { return chunk ^ (row & 7) ^ ((row >> 3) & 1); }
+__device__ __forceinline__ int swz(int row, int chunk) { return row * TK + 8 * swz_pos(row, chunk); }
+
+// SMALLG: group_k < 64 (grouped accumulation with group_k 16 or 32, or group
+// partials), GS = group_k / 16 steps per group; otherwise SPG = group_k / 64
+// slices per group (K is a multiple of group_k)
+template <int MODE, int GN, bool SMALLG, int GS, int SPG>
+__global__ __launch_bounds__(NT, 1) void kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ W,
+                                                uint16_t* __restrict__ C, float* __restrict__ P, int M, int N, int K,
+                                                int gk, int tiles_m, int tiles_n) {
+    __shared__ __attribute__((aligned(1024))) uint16_t sA0[SLICE];
+    __shared__ __attribute__((aligned(1024))) uint16_t sW0[SLICE];
+    __shared__ __attribute__((aligned(1024))) uint16_t sA1[SLICE];
+    __shared__ __attribute__((aligned(1024))) uint16_t sW1[SLICE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+
+    // ---- tile of this workgroup ----
+    const int T = tiles_m * tiles_n;
+    int u = blockIdx.x;
+    if ((T & 7) == 0) u = (u & 7) * (T >> 3) + (u >> 3);
+    const int band = 4 * tiles_n;
+    const int first = (u / band) * 4;
+    const int rows_in_band = min(tiles_m - first, 4);
+    const int within = u % band;
+    const int tm = first + within % rows_in_band;
+    const int tn = within / rows_in_band;
+    const int m0 = tm * TM, n0 = tn * TN;
+    const int wm = (wave >> 2) * 128;   // wave's rows in the tile
+    const int wn = (wave & 3) * 64;     // wave's columns in the tile
+
+    // ---- global -> LDS loads: wave w fills the 8-row groups w, w+8, w+16, w+24 of both slices ----
+    // Buffer loads: the resource starts at the tile's first row and this
+    // slice's first k, and its size ends at row M (N), so rows past the end
+    // read as zero.  The lane offsets are the same for A and W.
+    const int lrow = lane >> 3;
+    const int lchunk = (lane & 7) ^ lrow ^ (wave & 1);   // logical k chunk landing at this lane's LDS position
+    uint32_t voff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) voff[i] = (uint32_t)(((wave + 8 * i) * 8 + lrow) * K + 8 * lchunk) * 2u;
+    const int nkt = K / TK;
+    auto issue = [&](int kt, uint16_t* la, uint16_t* lw) __attribute__((always_inline)) {
+        const int k0 = kt * TK;
+        const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(A + (int64_t)m0 * K + k0), 0, (int)(((int64_t)(M - m0) * K - k0) * 2), 0x00020000);
+        const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(W + (int64_t)n0 * K + k0), 0, (int)(((int64_t)(N - n0) * K - k0) * 2), 0x00020000);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, la + (wave + 8 * i) * 8 * TK, 16, (int)voff[i], 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, lw + (wave + 8 * i) * 8 * TK, 16, (int)voff[i], 0, 0, 0);
+        }
+    };
+
+    f16v acc[2][4];     // [column block][row block]; fp32 partials of the current K group
+    h2_t H[2][4][8];    // fp16 accumulators
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int p = 0; p < 8; ++p) H[i][j][p] = (h2_t){(_Float16)0.f, (_Float16)0.f};
+
+    int ks = 0;   // 16-wide k steps done (group index of the partial dump)
+    // end of a K group: fold the partials into H (or dump them); the next
+    // group's first MFMA starts from a zero accumulator
+    auto group_end = [&]() __attribute__((always_inline)) {
+        if constexpr (MODE == kPartial) {
+            const int g = (ks * 16 - 1) / gk;
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int m = m0 + wm + 32 * j + (lane & 31);
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int n = n0 + wn + 32 * i + 8 * (r / 4) + 4 * (lane >> 5) + (r & 3);
+                        if (m < M && n < N) P[((int64_t)g * M + m) * N + n] = acc[i][j][r];
+                    }
+                }
+        } else if constexpr (MODE != kFp32) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) fold_block<MODE, GN>(acc[i][j], H[i][j]);
+        }
+    };
+
+    // One 64-wide K slice from buffer BUF.  FRESH: the slice starts a K group;
+    // FOLD: it ends one.  With group_k 16 / 32 (SMALLG) groups of GS steps
+    // start and end inside the slice.
+    auto stage = [&](int kt, auto buf_tag, auto fresh_tag, auto fold_tag) __attribute__((always_inline)) {
+        constexpr int BUF = decltype(buf_tag)::value;
+        constexpr bool FRESH = decltype(fresh_tag)::value;
+        constexpr bool FOLD = decltype(fold_tag)::value;
+        const uint16_t* la = BUF ? sA1 : sA0;
+        const uint16_t* lw = BUF ? sW1 : sW0;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();                      // slice kt landed; the other buffer fully read
+        if (kt + 1 < nkt) issue(kt + 1, BUF ? sA0 : sA1, BUF ? sW0 : sW1);
+        // keep the prefetch ahead of this slice's compute: without the fence the
+        // scheduler sinks the loads past it and the next wait exposes their latency
+        __builtin_amdgcn_sched_barrier(0);
+        // this lane's rows: wn + 32 i + lane % 32 of W, wm + 32 j + lane % 32 of A (row % 16 == lane % 16)
+        const char* lwb = reinterpret_cast<const char*>(lw) + (wn + (lane & 31)) * (TK * 2);
+        const char* lab = reinterpret_cast<const char*>(la) + (wm + (lane & 31)) * (TK * 2);
+#pragma unroll
+        for (int s = 0; s < TK / 16; ++s) {
+            const int cs = swz_pos(lane & 15, 2 * s + (lane >> 5)) << 4;   // swizzled chunk, bytes
+            h8 bop[2], aop[4];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) bop[i] = *reinterpret_cast<const h8*>(lwb + i * 32 * (TK * 2) + cs);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) aop[j] = *reinterpret_cast<const h8*>(lab + j * 32 * (TK * 2) + cs);
+            const bool zero = SMALLG ? (s % GS == 0) : (FRESH && s == 0);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bop[i], aop[j], zero ? (f16v){} : acc[i][j],
+                                                                       0, 0, 0);
+            if constexpr (SMALLG) {
+                if (s % GS == GS - 1) {
+                    ks += GS;
+                    group_end();
+                }
+            }
+        }
+        if constexpr (!SMALLG) {
+            ks += TK / 16;
+            if constexpr (FOLD) group_end();
+        }
+    };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+
+    issue(0, sA0, sW0);
+    int kt = 0;
+    if constexpr (MODE == kFp32) {   // one group over all of K
+        stage(0, B0{}, T_{}, F_{});
+        for (kt = 1; kt + 1 < nkt; kt += 2) {
+            stage(kt, B1{}, F_{}, F_{});
+            stage(kt + 1, B0{}, F_{}, F_{});
+        }
+        if (kt < nkt) stage(kt, B1{}, F_{}, F_{});
+    } else if constexpr (SMALLG || SPG == 1) {
+        for (; kt + 1 < nkt; kt += 2) {
+            stage(kt, B0{}, T_{}, T_{});
+            stage(kt + 1, B1{}, T_{}, T_{});
+        }
+        if (kt < nkt) stage(kt, B0{}, T_{}, T_{});
+    } else if constexpr (SPG == 2) {
+        for (; kt < nkt; kt += 2) {
+            stage(kt, B0{}, T_{}, F_{});
+            stage(kt + 1, B1{}, F_{}, T_{});
+        }
+    } else {
+        for (; kt < nkt; kt += 4) {
+            stage(kt, B0{}, T_{}, F_{});
+            stage(kt + 1, B1{}, F_{}, F_{});
+            stage(kt + 2, B0{}, F_{}, F_{});
+            stage(kt + 3, B1{}, F_{}, T_{});
+        }
+    }
+
+    if constexpr (MODE == kPartial) return;
+
+    // ---- store: each wave stages its 128x64 fp16 sub-tile (16 KB) in LDS, then writes full row segments ----
+    __syncthreads();
+    uint16_t* st = (wave < 2 ? sA0 : wave < 4 ? sW0 : wave < 6 ? sA1 : sW1) + (wave & 1) * (128 * 64);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                h2_t lo, hi;
+                if constexpr (MODE == kFp32) {
+                    lo = cvt2(acc[i][j][4 * q], acc[i][j][4 * q + 1]);
+                    hi = cvt2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+                } else {
+                    lo = H[i][j][2 * q];
+                    hi = H[i][j][2 * q + 1];
+                }
+                const int row = 32 * j + (lane & 31);
+                *reinterpret_cast<uint2*>(st + swz(row, 4 * i + q) + 4 * (lane >> 5)) =
+                    make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+            }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+        const int id = lane + 64 * t;
+        const int row = id >> 3, ch = id & 7;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(st + swz(row, ch));
+        const int m = m0 + wm + row, n = n0 + wn + 8 * ch;
+        if (m < M && n < N) *reinterpret_cast<u32x4*>(C + (int64_t)m * N + n) = v;
+    }
+}
+
+template <int MODE, int GN>
+void launch(const void* A, const void* W, void* C, float* P, int M, int N, int K, int gk, hipStream_t st) {
+    const int tm = (M + TM - 1) / TM, tn = (N + TN - 1) / TN;
+    const dim3 grid(tm * tn), block(NT);
+#define T256_LAUNCH(SM, GS_, SPG_)                                                                              \
+    hipLaunchKernelGGL((kernel<MODE, GN, SM, GS_, SPG_>), grid, block, 0, st, (const uint16_t*)A,              \
+                       (const uint16_t*)W, (uint16_t*)C, P, M, N, K, gk, tm, tn)
+    if constexpr (MODE == kFp32) {
+        T256_LAUNCH(false, 4, 1);
+    } else {
+        if (gk == 64) T256_LAUNCH(false, 4, 1);
+        else if (gk == 128) T256_LAUNCH(false, 4, 2);
+        else T256_LAUNCH(false, 4, 4);
+    }
+#undef T256_LAUNCH
+}
+
+}  // namespace t256
+
+int launch_tile256(int mode, int gn, const void* A, const void* B, void* C, float* P, int M, int N, int K, int gk,
+                   int b_is_nk, hipStream_t st) {
+    using namespace t256;
+    if (!b_is_nk || K % TK != 0 || N % 8 != 0 || M < 1 || N < 1) return 0;
+    // group_k 16 / 32 (grouped accumulation, group partials) stay on the 128x128 kernel
+    if (mode != kFp32 && (K % gk != 0 || (gk != 64 && gk != 128 && gk != 256))) return 0;
+    if (((uintptr_t)A | (uintptr_t)B | (uintptr_t)C) % 16 != 0) return 0;
+    // 32-bit element offsets inside the kernel
+    if ((int64_t)M * K >= (1ll << 31) || (int64_t)N * K >= (1ll << 31)) return 0;
+    if (mode == kFp32) gk = K;
+    switch (mode) {
+        case kGrouped: launch<kGrouped, 4>(A, B, C, P, M, N, K, gk, st); return 1;
+        case kFp32: launch<kFp32, 4>(A, B, C, P, M, N, K, gk, st); return 1;
+        case kPartial: launch<kPartial, 4>(A, B, C, P, M, N, K, gk, st); return 1;
+        case kInt8:
+            switch (gn) {
+                case 4: launch<kInt8, 4>(A, B, C, P, M, N, K, gk, st); return 1;
+                case 8: launch<kInt8, 8>(A, B, C, P, M, N, K, gk, st); return 1;
+                case 16: launch<kInt8, 16>(A, B, C, P, M, N, K, gk, st); return 1;
+                case 32: launch<kInt8, 32>(A, B, C, P, M, N, K, gk, st); return 1;
+            }
+            return 0;
+        case kFp8:
+            switch (gn) {
+                case 4: launch<kFp8, 4>(A, B, C, P, M, N, K, gk, st); return 1;
+                case 8: launch<kFp8, 8>(A, B, C, P, M, N, K, gk, st); return 1;
+                case 16: launch<kFp8, 16>(A, B, C, P, M, N, K, gk, st); return 1;
+                case 32: launch<kFp8, 32>(A, B, C, P, M, N, K, gk, st); return 1;
+            }
+            return 0;
+    }
+    return 0;
+}
+
+}  // namespace hbq_gemm

@@ -191,3 +191,29 @@ def test_fp16accum_matmul_module(gpu, oracle):
         FP16AccumMatMul(256, 32)(x, W.to(gpu))
     with pytest.raises(ValueError):
         FP16AccumMatMul(128, 64)(x, W.to(gpu))
+
+
+@pytest.mark.parametrize("op", ["fp32", "grouped", "mxint8", "mxfp8"])
+def test_kn_and_nk_layouts_bit_identical(gpu, op):
+    """B[K,N] through the 128x128 kernel, W[N,K] through the 256x256 kernel, and B[K,N]
+    transposed to W[N,K] by the op: the same bits (same MFMA sequence per output)."""
+    from hbq_amd import blockquant_ext as ext
+    M, K, N = 320, 1024, 384
+    A = synth(M, K, 41, "f16").to(gpu)
+    B = synth(K, N, 42, "f16", std=0.02, outliers=0, laplace_frac=0).to(gpu)
+    W = B.t().contiguous()
+    call = {"fp32": lambda b, nk: ext.gemm_fp32_accum(A, b, b_is_nk=nk),
+            "grouped": lambda b, nk: ext.gemm_fp16_grouped_accum(A, b, 128, b_is_nk=nk),
+            "mxint8": lambda b, nk: ext.gemm_blockquant_mxint8(A, b, 128, 32, b_is_nk=nk),
+            "mxfp8": lambda b, nk: ext.gemm_blockquant_mxfp8(A, b, 64, 16, b_is_nk=nk)}[op]
+    old = ext.TRANSPOSE_MIN_MNK
+    try:
+        ext.TRANSPOSE_MIN_MNK = 1 << 62
+        kn = call(B, False)
+        ext.TRANSPOSE_MIN_MNK = 0
+        kn_t = call(B, False)
+    finally:
+        ext.TRANSPOSE_MIN_MNK = old
+    nk = call(W, True)
+    assert torch.equal(kn.view(torch.int16), nk.view(torch.int16))
+    assert torch.equal(kn_t.view(torch.int16), nk.view(torch.int16))
