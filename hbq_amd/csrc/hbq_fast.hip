@@ -132,16 +132,6 @@ __global__ void build_lut_kernel(int slot, FastParams p) {
     }
 }
 
-// max over the 8 lanes of a block with DPP: swap neighbours, swap pairs, mirror halves of 8
-__device__ __forceinline__ uint32_t max8_dpp(uint32_t v) {
-    uint32_t o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xf, 0xf, true);   // quad_perm [1,0,3,2]
-    v = v > o ? v : o;
-    o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xf, 0xf, true);            // quad_perm [2,3,0,1]
-    v = v > o ? v : o;
-    o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xf, 0xf, true);           // row_half_mirror
-    return v > o ? v : o;
-}
-
 // Block 128 (8 lanes x 16 elements).  Per-wave magnitude tables, laid out
 // [scheme][candidate][block-in-wave][level] with rows padded by one entry so
 // that the eight blocks of a wave fall on different LDS banks.

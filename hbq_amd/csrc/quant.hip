@@ -14,6 +14,7 @@
 #include "hbq_capi_internal.h"
 #include "hbq_fast.h"
 #include "quant_common.h"
+#include "hbq_block.h"
 
 namespace hbq {
 
@@ -102,104 +103,30 @@ __global__ __launch_bounds__(kThreads) void hbq_qdq_kernel(const typename T::sto
     const Locate L = locate(lpb_log2, nblk_row, nb, block);
     const int lpb = 1 << lpb_log2;
     const int lane = (int)(threadIdx.x & 63);
-    const int lane_base = lane - L.li;
 
     float xv[kV];
     load_lane<T>(x, L, cols, xv, ragged);
 
-    uint32_t m = 0;
-#pragma unroll
-    for (int i = 0; i < kV; ++i) {
-        uint32_t b = f2bits(xv[i]) & 0x7fffffffu;
-        m = m > b ? m : b;
-    }
-    const float amax = bits2f(group_max_bits(m, lpb));
-
-    float l1[S];
-    float dsel[S][kV], sqsel[S][kV];
-    uint32_t csel[S][kV];
-    int jsel[S][NSUBL];
-
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-        l1[s] = scale_quant<T>(T::round(amax / p.em[s]), p.sf);
-        const float rl1 = 1.0f / l1[s];
-        float t[kV];
-#pragma unroll
-        for (int i = 0; i < kV; ++i) t[i] = div_T<T>(xv[i], l1[s], rl1);
-        float best[NSUBL];
-        for (int j = 0; j < p.J; ++j) {
-            const float l2 = p.l2[j][s], rl2 = p.rl2[j][s];
-            float dj[kV], sqj[kV];
-            uint32_t cj[kV];
-#pragma unroll
-            for (int i = 0; i < kV; ++i) {
-                float u = (l2 == 1.0f) ? t[i] : div_T<T>(t[i], l2, rl2);
-                float q = elem_quant<T, M>(u, cj[i]);
-                float d = T::round(T::round(q * l2) * l1[s]);
-                float e = T::round(xv[i] - d);
-                dj[i] = d;
-                sqj[i] = T::round(e * e);
-            }
-#pragma unroll
-            for (int sb = 0; sb < NSUBL; ++sb) {
-                constexpr int n = L2B <= kV ? L2B : kV;
-                float acc = 0.f;
-#pragma unroll
-                for (int i = 0; i < n; ++i) acc += sqj[sb * n + i];
-                if (LPS > 1) {
-                    // sub-block spans LPS lanes: fold their 16-term sums in lane order
-                    const int first = lane - (L.li % LPS);
-                    float tot = __shfl(acc, first, 64);
-                    for (int k = 1; k < LPS; ++k) tot += __shfl(acc, first + k, 64);
-                    acc = tot;
-                }
-                const float sse = T::round(acc);
-                if (j == 0 || better(sse, best[sb])) {
-                    best[sb] = sse;
-                    jsel[s][sb] = j;
-#pragma unroll
-                    for (int i = 0; i < n; ++i) {
-                        dsel[s][sb * n + i] = dj[sb * n + i];
-                        sqsel[s][sb * n + i] = sqj[sb * n + i];
-                        csel[s][sb * n + i] = cj[sb * n + i];
-                    }
-                }
-            }
-        }
-    }
-
-    int sstar = 0;
-    if constexpr (S == 2) {
-        float e0 = T::round(block_row_sum(sqsel[0], L.li, lpb, lane_base));
-        float e1 = T::round(block_row_sum(sqsel[S - 1], L.li, lpb, lane_base));
-        sstar = better(e1, e0) ? 1 : 0;
-    }
-
     float out[kV];
     uint32_t cout[kV];
-#pragma unroll
-    for (int i = 0; i < kV; ++i) {
-        out[i] = (S == 2 && sstar) ? dsel[S - 1][i] : dsel[0][i];
-        cout[i] = (S == 2 && sstar) ? csel[S - 1][i] : csel[0][i];
-    }
+    float l1sel;
+    int sstar;
+    int jsel[NSUBL];
+    hbq_block<T, M, L2B, S>(xv, L.li, lpb, lane, p, out, cout, l1sel, sstar, jsel);
     store_lane<T>(y, L, cols, out, ragged);
     if (!L.valid) return;
     store_codes<M>(codes, L.row, cols, L.c0, cout, ragged);
     if (L.li == 0) {
-        if (l1_out) l1_out[L.gb] = T::store((S == 2 && sstar) ? l1[S - 1] : l1[0]);
+        if (l1_out) l1_out[L.gb] = T::store(l1sel);
         if (sch_out) sch_out[L.gb] = (uint8_t)sstar;
     }
     if (l2i_out) {
         const int nsub_blk = block / L2B;
         if (L2B <= kV) {
 #pragma unroll
-            for (int sb = 0; sb < NSUBL; ++sb) {
-                l2i_out[L.gb * nsub_blk + (L.li * kV) / L2B + sb] =
-                        (uint8_t)((S == 2 && sstar) ? jsel[S - 1][sb] : jsel[0][sb]);
-            }
+            for (int sb = 0; sb < NSUBL; ++sb) l2i_out[L.gb * nsub_blk + (L.li * kV) / L2B + sb] = (uint8_t)jsel[sb];
         } else if ((L.li % LPS) == 0) {
-            l2i_out[L.gb * nsub_blk + (L.li * kV) / L2B] = (uint8_t)((S == 2 && sstar) ? jsel[S - 1][0] : jsel[0][0]);
+            l2i_out[L.gb * nsub_blk + (L.li * kV) / L2B] = (uint8_t)jsel[0];
         }
     }
 }

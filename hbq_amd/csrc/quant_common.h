@@ -106,6 +106,16 @@ __device__ __forceinline__ uint32_t group_max_bits(uint32_t v, int lpb) {
     return v;
 }
 
+// max over the 8 lanes of a block with DPP: swap neighbours, swap pairs, mirror halves of 8
+__device__ __forceinline__ uint32_t max8_dpp(uint32_t v) {
+    uint32_t o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xf, 0xf, true);   // quad_perm [1,0,3,2]
+    v = v > o ? v : o;
+    o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xf, 0xf, true);            // quad_perm [2,3,0,1]
+    v = v > o ? v : o;
+    o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xf, 0xf, true);           // row_half_mirror
+    return v > o ? v : o;
+}
+
 struct Locate {
     int64_t gb;     // global block index
     int li;         // lane within the block
