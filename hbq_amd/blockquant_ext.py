@@ -47,7 +47,10 @@ def _prep(A, B, b_is_nk, group_k=64):
     M, K = A.shape
     N = B.size(0) if b_is_nk else B.size(1)
     if not b_is_nk and M * N * K >= TRANSPOSE_MIN_MNK and K % 64 == 0 and N % 8 == 0 and group_k >= 64:
-        B, b_is_nk = B.t().contiguous(), True
+        B = B.contiguous()
+        W = torch.empty((N, K), dtype=B.dtype, device=B.device)
+        _call(_lib.lib().hbq_transpose16, _lib.ptr(B), _lib.ptr(W), K, N, _lib.stream_of(B))
+        B, b_is_nk = W, True
     else:
         B = B.contiguous()
     C = torch.empty((M, N), dtype=torch.float16, device=A.device)

@@ -270,6 +270,55 @@ __global__ __launch_bounds__(256) void gemm_fp16acc_kernel(const uint16_t* __res
         }
 }
 
+// ---- 16-bit transpose (B[K,N] -> W[N,K] for the 256x256 kernel) ----------
+// 64x64 tiles through LDS: 16-byte loads along the source rows, 16-byte stores
+// along the destination rows.
+constexpr int TT = 64;
+__global__ __launch_bounds__(256) void transpose16_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                                          int64_t rows, int64_t cols) {
+    __shared__ uint16_t t[TT][TT + 2];
+    const int64_t r0 = (int64_t)blockIdx.y * TT, c0 = (int64_t)blockIdx.x * TT;
+    const bool vec = (cols % 8 == 0) && (rows % 8 == 0) && (((uintptr_t)src | (uintptr_t)dst) % 16 == 0);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int id = threadIdx.x + 256 * k;          // 512 chunks of 8 halfs
+        const int rr = id / 8, cc = (id % 8) * 8;
+        const int64_t r = r0 + rr, c = c0 + cc;
+        uint16_t v[8];
+        if (vec && r < rows && c + 8 <= cols) {
+            const u32x4 q = *reinterpret_cast<const u32x4*>(src + r * cols + c);
+            const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = (uint16_t)(w[e / 2] >> (16 * (e % 2)));
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = (r < rows && c + e < cols) ? src[r * cols + c + e] : (uint16_t)0;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t[rr][cc + e] = v[e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int id = threadIdx.x + 256 * k;
+        const int cr = id / 8, rc = (id % 8) * 8;       // destination row (source column), 8 source rows
+        const int64_t dr = c0 + cr, dc = r0 + rc;
+        uint16_t v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = t[rc + e][cr];
+        if (dr >= cols) continue;
+        if (vec && dc + 8 <= rows) {
+            *reinterpret_cast<u32x4*>(dst + dr * rows + dc) =
+                (u32x4){(uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16),
+                        (uint32_t)v[4] | ((uint32_t)v[5] << 16), (uint32_t)v[6] | ((uint32_t)v[7] << 16)};
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (dc + e < rows) dst[dr * rows + dc + e] = v[e];
+        }
+    }
+}
+
 }  // namespace hbq_gemm
 
 using namespace hbq_gemm;
@@ -401,6 +450,18 @@ int hbq_gemm_blockquant_mxint8(const void* A, const void* B, void* C, int64_t M,
 int hbq_gemm_blockquant_mxfp8(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int group_k,
                               int group_n, int b_is_nk, void* stream) {
     return psum_common(kFp8, A, B, C, M, N, K, group_k, group_n, b_is_nk, stream, "gemm_blockquant_mxfp8");
+}
+
+int hbq_transpose16(const void* src, void* dst, int64_t rows, int64_t cols, void* stream) {
+    hbq_clear_error();
+    if (rows < 0 || cols < 0) return hbq_fail(HBQ_ERR_INVALID, "negative shape");
+    if (rows == 0 || cols == 0) return 0;
+    if (src == nullptr || dst == nullptr) return hbq_fail(HBQ_ERR_INVALID, "null tensor pointer");
+    const int64_t gx = (cols + TT - 1) / TT, gy = (rows + TT - 1) / TT;
+    if (gx > 0x7fffffff || gy > 65535) return hbq_fail(HBQ_ERR_INVALID, "tensor too large for one launch");
+    hipLaunchKernelGGL(transpose16_kernel, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)src, (uint16_t*)dst, rows, cols);
+    return hbq_check_launch("transpose16");
 }
 
 int hbq_gemm_group_partials(const void* A, const void* B, void* P, int64_t M, int64_t N, int64_t K, int group_k,

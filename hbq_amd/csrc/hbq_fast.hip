@@ -456,8 +456,11 @@ int launch_fast(const void* x, void* y, void* l1, void* l2i, void* sch, void* co
         return 0;
     const int64_t blocks_per_wg = kThreads >> lpb_log2;
     const int64_t ntiles = (nb + blocks_per_wg - 1) / blocks_per_wg;
-    int64_t grid = (int64_t)g_cus[dev] * per_cu;
-    if (grid > ntiles) grid = ntiles;
+    // as many rounds as the resident workgroups need, with the tiles spread evenly over
+    // them (a last round with few tiles would leave most of the chip idle)
+    const int64_t resident = (int64_t)g_cus[dev] * per_cu;
+    const int64_t rounds = (ntiles + resident - 1) / resident;
+    const int64_t grid = (ntiles + rounds - 1) / rounds;
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), lds, st, (const St*)x, (St*)y, (St*)l1,
                        (uint8_t*)l2i, (uint8_t*)sch, (uint8_t*)codes, nb, slot, p);
     return 1;

@@ -141,6 +141,11 @@ int hbq_gemm_blockquant_mxfp8(const void *A, const void *B, void *C, int64_t M, 
 int hbq_gemm_group_partials(const void *A, const void *B, void *P, int64_t M, int64_t N, int64_t K, int group_k,
                             int b_is_nk, void *stream);
 
+/* No reference counterpart: dst[cols, rows] = src[rows, cols]^T for 16-bit
+ * elements.  The blockquant_ext front end uses it to hand a B[K,N] operand to
+ * the W[N,K] kernels. */
+int hbq_transpose16(const void *src, void *dst, int64_t rows, int64_t cols, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -217,3 +217,15 @@ def test_kn_and_nk_layouts_bit_identical(gpu, op):
     nk = call(W, True)
     assert torch.equal(kn.view(torch.int16), nk.view(torch.int16))
     assert torch.equal(kn_t.view(torch.int16), nk.view(torch.int16))
+
+
+@pytest.mark.parametrize("shape", [(1, 1), (7, 130), (64, 64), (200, 72), (4096, 136), (96, 1000)])
+def test_transpose16(gpu, shape):
+    """The B[K,N] -> W[N,K] helper: exact copy, ragged and unaligned shapes included."""
+    from hbq_amd import _lib
+    rows, cols = shape
+    g = torch.Generator(device=gpu).manual_seed(rows * 1000 + cols)
+    src = torch.randint(-32768, 32767, (rows, cols), device=gpu, dtype=torch.int32, generator=g).to(torch.int16)
+    dst = torch.empty((cols, rows), device=gpu, dtype=torch.int16)
+    _lib.check(_lib.lib().hbq_transpose16(_lib.ptr(src), _lib.ptr(dst), rows, cols, _lib.stream_of(src)))
+    assert torch.equal(dst, src.t())
