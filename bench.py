@@ -171,6 +171,53 @@ def gemm_extra(dev, cases=GEMM_CASES, iters=10):
     return out
 
 
+# config/hbq_a_kv.yaml (HBQ-A weights and activations, post-RoPE Q, K and V
+# caches in 4 bit, attention weights quantized, fp32 accumulation)
+HBQ_A_KV = {
+    "quantization": {"xqtype": "hbq", "wqtype": "hbq", "quant_post_rope_q": True, "quant_k_cache": True,
+                     "quant_v_cache": True, "quant_4b_kv": True, "quant_attn_wgt": True,
+                     "quant_attn_wgt_use_quant_kernel": False},
+    "block_quant": {"act_ebit": 2, "act_mbit": 2, "act_block_size": 128, "act_sc_ebit": 5, "act_sc_mbit": 3,
+                    "wgt_ebit": 2, "wgt_mbit": 1, "wgt_block_size": 128, "wgt_sc_ebit": 5, "wgt_sc_mbit": 3,
+                    "wgt_l2_sc_bit": 2, "wgt_l2_block_size": 8, "wgt_l2_scheme": "Mix", "act_l2_sc_bit": 2,
+                    "act_l2_block_size": 8, "act_l2_scheme": "SIG-1", "wgt_per_tensor_scale": False,
+                    "act_per_tensor_scale": False, "scale_allow_subnormal": False, "qk_mx_round": False},
+    "accumulation": {"type": "fp32"},
+}
+
+
+def prefill_extra(dev, T=2048, iters=3):
+    """one prefill of T tokens through Llama-3-8B (32 layers, random N(0, 0.02)
+    weights, fp16) with the HBQ-A + KV quantization points; weights quantized once beforehand."""
+    from hbq_amd.llama import LlamaConfig, LlamaForCausalLM
+    from hbq_amd.ptq import PTQ
+    cfg = LlamaConfig()
+    with torch.device(dev):
+        m = LlamaForCausalLM(cfg).half()
+    m.random_init_(seed=4)
+    p = PTQ(HBQ_A_KV, m)
+    p.inject_quantizers()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    p.static_quant_wgt()
+    torch.cuda.synchronize()
+    t_wq = time.perf_counter() - t0
+    ids = torch.randint(0, cfg.vocab_size, (1, T), device=dev, generator=torch.Generator(device=dev).manual_seed(4))
+    with torch.no_grad():
+        m(ids)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            out = m(ids)
+        torch.cuda.synchronize()
+    t = (time.perf_counter() - t0) / iters
+    assert torch.isfinite(out).all()
+    del m, out
+    torch.cuda.empty_cache()
+    return {"cfg4_prefill_ms": round(t * 1e3, 2), "cfg4_prefill_tokens_per_s": round(T / t, 1),
+            "cfg4_weight_quant_ms": round(t_wq * 1e3, 1)}
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -217,6 +264,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only: skip the extra formats, GEMMs and CPU leg")
     ap.add_argument("--gemm-only", action="store_true", help="print only the GEMM measurements")
+    ap.add_argument("--prefill-only", action="store_true", help="print only the configs[4] prefill measurement")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the HBQ hot path here has no multi-GPU mode (--gpus {args.gpus} "
@@ -227,6 +275,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.gemm_only:
         print(json.dumps(gemm_extra(dev)))
+        return
+    if args.prefill_only:
+        print(json.dumps(prefill_extra(dev)))
         return
 
     x_cpu = config1_tensor()
@@ -271,6 +322,7 @@ def main():
             t = HipTimer().run(s4, 100)
             extra[f"{name}_fp16_GBs"] = round(n * mx_bytes_per_elem(c) / t / 1e9, 1)
         extra.update(gemm_extra(dev))
+        extra.update(prefill_extra(dev))
     # device-to-device copy of the same tensor: the measured bandwidth ceiling, and the
     # known-size kernel that scales the HBM byte counters
     dst = torch.empty_like(x)

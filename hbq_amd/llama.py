@@ -1,0 +1,195 @@
+"""A Llama decoder with the reference's quantization points, for the prefill
+workload (Llama-3-8B shapes, random weights).
+
+Mirrors the quantized modules of src/module.py that the hot path serves:
+_QBaseLinear projections (src/module.py:20-67), QLlamaAttention.forward with
+its post-RoPE Q, K-cache, V-cache (quantized along tokens) and attention-weight
+quantizers (src/module.py:93-199), and QLlamaMLP (src/module.py:547-569).  The
+surrounding Llama pieces (RMSNorm, rotary embedding, repeat_kv, the residual
+stream) follow the Hugging Face Llama definition the reference patches; they
+are plain torch code, in fp16 as the reference runs them.  `PTQ` (hbq_amd.ptq)
+injects the quantizers, quantizes the weights and installs the accumulation
+kernel on this model exactly as on the reference's.
+"""
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+
+from .module import _QBaseLinear, deferred_finite_checks, same_quantizer
+
+
+@dataclass
+class LlamaConfig:
+    hidden_size: int = 4096
+    intermediate_size: int = 14336
+    num_hidden_layers: int = 32
+    num_attention_heads: int = 32
+    num_key_value_heads: int = 8
+    vocab_size: int = 128256
+    rms_norm_eps: float = 1e-5
+    rope_theta: float = 500000.0
+    model_type: str = "llama"
+    _name_or_path: str = "llama-3-8b (random weights)"
+
+    @property
+    def head_dim(self):
+        return self.hidden_size // self.num_attention_heads
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, n, eps):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(n))
+        self.eps = eps
+
+    def forward(self, x):
+        dt = x.dtype
+        h = x.float()
+        h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + self.eps)
+        return self.weight * h.to(dt)
+
+
+def rotary(cfg, T, device):
+    """cos, sin [T, head_dim] (fp32) of the rotary embedding."""
+    d = cfg.head_dim
+    inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, d, 2, device=device, dtype=torch.float32) / d))
+    f = torch.outer(torch.arange(T, device=device, dtype=torch.float32), inv)
+    emb = torch.cat((f, f), dim=-1)
+    return emb.cos(), emb.sin()
+
+
+def _rotate_half(x):
+    h = x.shape[-1] // 2
+    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
+def apply_rope(q, k, cos, sin):
+    cos = cos.to(q.dtype)[None, None]
+    sin = sin.to(q.dtype)[None, None]
+    return q * cos + _rotate_half(q) * sin, k * cos + _rotate_half(k) * sin
+
+
+class QLlamaAttention(nn.Module):
+    """Attention with the reference's quantization points (src/module.py:93-199)."""
+
+    def __init__(self, cfg: LlamaConfig):
+        super().__init__()
+        self.cfg = cfg
+        h, d = cfg.hidden_size, cfg.head_dim
+        self.num_heads, self.num_key_value_heads, self.head_dim = cfg.num_attention_heads, cfg.num_key_value_heads, d
+        self.q_proj = _QBaseLinear(h, self.num_heads * d, bias=False)
+        self.k_proj = _QBaseLinear(h, self.num_key_value_heads * d, bias=False)
+        self.v_proj = _QBaseLinear(h, self.num_key_value_heads * d, bias=False)
+        self.o_proj = _QBaseLinear(self.num_heads * d, h, bias=False)
+        self.quant_attn_wgt = False
+        self.quant_post_rope_q = False
+        self.quant_k_cache = False
+        self.quant_v_cache = False
+        self.kv_quantizer = None
+        self.attn_wgt_quantizer = None
+
+    def manual_sdpa(self, q, k, v):
+        """Causal softmax(q k^T / sqrt(d)) v with the attention weights quantized after the
+        softmax (src/module.py:93-117)."""
+        T = q.shape[-2]
+        scale = 1.0 / math.sqrt(q.shape[-1])
+        s = torch.matmul(q, k.transpose(-2, -1).contiguous()) * scale
+        mask = torch.full((T, T), float("-inf"), device=q.device, dtype=s.dtype).triu(1)
+        s = s + mask
+        p = torch.softmax(s, dim=-1)
+        if self.quant_attn_wgt:
+            p = self.attn_wgt_quantizer.q(p)
+        return torch.matmul(p, v), p
+
+    def forward(self, x, cos, sin):
+        b, T, _ = x.shape
+        qp, kp, vp = self.q_proj, self.k_proj, self.v_proj
+        if same_quantizer(qp.aq, kp.aq) and same_quantizer(qp.aq, vp.aq):
+            # q, k and v quantize the same input with the same function: quantize it once
+            xq = qp.aq(x)
+            q, k, v = qp.forward_quantized(xq), kp.forward_quantized(xq), vp.forward_quantized(xq)
+        else:
+            q, k, v = qp(x), kp(x), vp(x)
+        q = q.view(b, T, self.num_heads, self.head_dim).transpose(1, 2)
+        k = k.view(b, T, self.num_key_value_heads, self.head_dim).transpose(1, 2)
+        v = v.view(b, T, self.num_key_value_heads, self.head_dim).transpose(1, 2)
+        q, k = apply_rope(q, k, cos, sin)
+        if self.quant_post_rope_q:
+            q = self.q_proj.aq.q(q)
+        if self.quant_k_cache:
+            k = self.kv_quantizer.q(k)                        # (batch, heads, tokens, head_dim)
+        if self.quant_v_cache:
+            # V is quantized along the tokens: the following product is P @ V
+            v = self.kv_quantizer.q(v.transpose(-1, -2).contiguous()).transpose(-1, -2).contiguous()
+        rep = self.num_heads // self.num_key_value_heads
+        k = k.repeat_interleave(rep, dim=1)
+        v = v.repeat_interleave(rep, dim=1)
+        out, _ = self.manual_sdpa(q.contiguous(), k.contiguous(), v.contiguous())
+        out = out.transpose(1, 2).contiguous().view(b, T, -1)
+        return self.o_proj(out)
+
+
+class QLlamaMLP(nn.Module):
+    """SiLU-gated MLP with quantized projections (src/module.py:547-569)."""
+
+    def __init__(self, cfg: LlamaConfig):
+        super().__init__()
+        self.gate_proj = _QBaseLinear(cfg.hidden_size, cfg.intermediate_size, bias=False)
+        self.up_proj = _QBaseLinear(cfg.hidden_size, cfg.intermediate_size, bias=False)
+        self.down_proj = _QBaseLinear(cfg.intermediate_size, cfg.hidden_size, bias=False)
+        self.quantizer_after_act_fn = None
+
+    def forward(self, x):
+        if same_quantizer(self.gate_proj.aq, self.up_proj.aq):
+            xq = self.gate_proj.aq(x)     # gate and up quantize the same input identically
+            gate, up = self.gate_proj.forward_quantized(xq), self.up_proj.forward_quantized(xq)
+        else:
+            gate, up = self.gate_proj(x), self.up_proj(x)
+        g = torch.nn.functional.silu(gate)
+        if self.quantizer_after_act_fn is not None:
+            g = self.quantizer_after_act_fn.q(g)
+        return self.down_proj(g * up)
+
+
+class DecoderLayer(nn.Module):
+    def __init__(self, cfg):
+        super().__init__()
+        self.input_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+        self.self_attn = QLlamaAttention(cfg)
+        self.post_attention_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+        self.mlp = QLlamaMLP(cfg)
+
+    def forward(self, x, cos, sin):
+        x = x + self.self_attn(self.input_layernorm(x), cos, sin)
+        return x + self.mlp(self.post_attention_layernorm(x))
+
+
+class LlamaForCausalLM(nn.Module):
+    def __init__(self, cfg: LlamaConfig):
+        super().__init__()
+        self.config = cfg
+        self.embed_tokens = nn.Embedding(cfg.vocab_size, cfg.hidden_size)
+        self.layers = nn.ModuleList([DecoderLayer(cfg) for _ in range(cfg.num_hidden_layers)])
+        self.norm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+        self.lm_head = _QBaseLinear(cfg.hidden_size, cfg.vocab_size, bias=False)
+
+    @torch.no_grad()
+    def random_init_(self, std=0.02, seed=0):
+        """N(0, std^2) weights (the benchmark has no checkpoint), unit norm weights."""
+        g = torch.Generator(device=self.embed_tokens.weight.device).manual_seed(seed)
+        for name, p in self.named_parameters():
+            if name.endswith("layernorm.weight") or name == "norm.weight":
+                p.fill_(1.0)
+            else:
+                p.normal_(0.0, std, generator=g)
+        return self
+
+    def forward(self, ids):
+        with deferred_finite_checks():
+            x = self.embed_tokens(ids)
+            cos, sin = rotary(self.config, ids.shape[1], ids.device)
+            for layer in self.layers:
+                x = layer(x, cos, sin)
+            return self.lm_head(self.norm(x))

@@ -7,11 +7,52 @@ place, by `PTQ.static_quant_linear_weight`; `forward` quantizes the input, runs
 the GEMM (torch's `F.linear` when `ops` is None, as in the reference), raises on
 a non-finite result and applies `yq`.
 """
+import contextlib
+
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
 from .quantizer import _QBase
+
+# Active deferred-check scopes (see deferred_finite_checks).
+_DEFERRED = []
+
+
+@contextlib.contextmanager
+def deferred_finite_checks():
+    """Inside this scope _QBaseLinear records each output's finiteness on the device
+    instead of synchronizing per layer, and the scope raises on exit if any output was
+    not finite.  The reference raises per layer (src/module.py:51-66); the error still
+    reaches the caller before the forward returns, without a host sync per layer."""
+    flags = []
+    _DEFERRED.append(flags)
+    try:
+        yield
+    finally:
+        _DEFERRED.pop()
+    if flags:
+        ok = torch.stack([f for _, f in flags]).cpu()
+        for (mod, _), good in zip(flags, ok.tolist()):
+            if not good:
+                raise RuntimeError(
+                    f"Non-finite output from {type(mod).__name__}({mod.in_features} -> {mod.out_features}) "
+                    f"(found after the forward).\n"
+                    f"  activation quantizer: {type(mod.aq).__name__}\n"
+                    f"  weight quantizer:     {type(mod.wq).__name__}\n"
+                    f"  matmul:               {type(mod.ops).__name__ if mod.ops is not None else 'F.linear'}\n"
+                    "The quantization format cannot represent this layer's dynamic range: check the element and "
+                    "scale exponent bits and the block size of the quantization config.")
+
+
+def same_quantizer(a, b):
+    """True when two quantizers compute the same function (same class and settings), so one
+    quantized copy of an input can serve both."""
+    if type(a) is not type(b):
+        return False
+    keys = ("ebit", "mbit", "sc_ebit", "sc_mbit", "block_size", "per_tensor_scale", "scale_allow_subnormal",
+            "use_round", "use_ceil", "l2_block_size", "l2_sc_bit", "l2_scheme")
+    return all(getattr(a, k, None) == getattr(b, k, None) for k in keys)
 
 
 class _QBaseLinear(nn.Linear):
@@ -26,7 +67,10 @@ class _QBaseLinear(nn.Linear):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         # the weight was quantized in place before inference (src/ptq.py:338-358)
-        xq = self.aq(x)
+        return self.forward_quantized(self.aq(x))
+
+    def forward_quantized(self, xq: torch.Tensor) -> torch.Tensor:
+        """forward() on an input already quantized by a quantizer equal to self.aq."""
         if self.ops is None:
             y = F.linear(xq, self.weight, self.bias)
         else:
@@ -36,6 +80,9 @@ class _QBaseLinear(nn.Linear):
 
     def _check_finite(self, y):
         # src/module.py:51-66: a non-finite GEMM output is an error of the format choice
+        if _DEFERRED:
+            _DEFERRED[-1].append((self, torch.isfinite(y).all()))
+            return
         if bool(torch.isfinite(y).all()):
             return
         ops_name = type(self.ops).__name__ if self.ops is not None else "F.linear"

@@ -1,0 +1,116 @@
+"""The Llama decoder with the reference's quantization points (src/module.py:93-199,
+547-569) driven by PTQ: structure on the CPU, kernels and quantization points on
+the GPU against the oracle."""
+import numpy as np
+import pytest
+import torch
+
+from hbq_amd import quantizer as Q
+from hbq_amd.llama import LlamaConfig, LlamaForCausalLM
+from hbq_amd.module import _QBaseLinear
+from hbq_amd.ptq import PTQ
+from helpers import mismatches, to_bits
+from test_ptq import hbq_cfg
+
+TINY = LlamaConfig(hidden_size=256, intermediate_size=512, num_hidden_layers=2, num_attention_heads=4,
+                   num_key_value_heads=2, vocab_size=1000)
+
+
+def test_structure_and_injection_cpu():
+    m = LlamaForCausalLM(TINY).random_init_()
+    p = PTQ(hbq_cfg(kv=True), m)
+    p.inject_quantizers()
+    a = m.layers[0].self_attn
+    assert a.quant_post_rope_q and a.quant_k_cache and a.quant_v_cache and a.quant_attn_wgt
+    assert isinstance(a.kv_quantizer, Q.HBQQuantizer) and a.kv_quantizer.mbit == 1
+    assert sum(isinstance(x, _QBaseLinear) for x in m.modules()) == 2 * 7 + 1
+    # unquantized forward (identity quantizers) on the CPU
+    m2 = LlamaForCausalLM(TINY).random_init_()
+    y = m2(torch.randint(0, 1000, (1, 16)))
+    assert y.shape == (1, 16, 1000) and torch.isfinite(y).all()
+
+
+@pytest.mark.gpu
+def test_quantization_points_match_oracle(gpu, oracle):
+    """Every quantizer call of a prefill (X of each linear, post-RoPE Q, K and V caches, the
+    attention weights) returns the oracle's result on the same input."""
+    print("llama quantization points", flush=True)
+    torch.manual_seed(0)
+    m = LlamaForCausalLM(TINY).random_init_().half().to(gpu)
+    p = PTQ(hbq_cfg(kv=True), m)
+    p.inject_quantizers()
+    p.static_quant_wgt()
+    calls = []
+    for mod in m.modules():
+        for attr in ("aq", "kv_quantizer", "attn_wgt_quantizer"):
+            qz = getattr(mod, attr, None)
+            if isinstance(qz, Q.HBQQuantizer) and not hasattr(qz, "_wrapped"):
+                orig = qz.q
+
+                def rec(x, _orig=orig, _qz=qz):
+                    y = _orig(x)
+                    calls.append((_qz, x.detach().clone(), y.detach().clone()))
+                    return y
+                qz.q = rec
+                qz._wrapped = True
+    ids = torch.randint(0, TINY.vocab_size, (1, 128), device=gpu)
+    with torch.no_grad():
+        out = m(ids)
+    assert torch.isfinite(out).all()
+    kinds = set()
+    for qz, x, y in calls:
+        xs = to_bits(x.reshape(-1, x.shape[-1]))
+        ref = oracle.hbq_qdq(xs, "f16", block_size=qz.block_size, ebit=qz.ebit, mbit=qz.mbit, sc_ebit=qz.sc_ebit,
+                             sc_mbit=qz.sc_mbit, l2_block_size=qz.l2_block_size, l2_sc_bit=qz.l2_sc_bit,
+                             l2_scheme=qz.l2_scheme)["y"]
+        assert mismatches(to_bits(y.reshape(-1, y.shape[-1])), ref, "f16") == 0
+        kinds.add((qz.mbit, tuple(x.shape[-2:]) if x.dim() == 4 else "x"))
+    # X of the projections (q/k/v and gate/up share one quantized copy), Q (E2M2), K and V
+    # (E2M1, V transposed: tokens last), P
+    assert len(calls) == TINY.num_hidden_layers * (4 + 4)
+    assert (1, (128, TINY.head_dim)) in kinds and (1, (TINY.head_dim, 128)) in kinds and (2, (128, 128)) in kinds
+
+
+@pytest.mark.gpu
+def test_prefill_fast_kernels_equal_generic(gpu):
+    """The same prefill with every quantizer forced onto the generic kernel: identical logits."""
+    from hbq_amd import _lib
+    print("llama prefill fast vs generic", flush=True)
+    m = LlamaForCausalLM(TINY).random_init_(seed=3).half().to(gpu)
+    p = PTQ(hbq_cfg(kv=True, acc={"type": "fp16_quant", "group_size": 128, "quant_block_size": 32}), m)
+    p.inject_quantizers()
+    p.static_quant_wgt()
+    p.replace_accum_kernel()
+    ids = torch.randint(0, TINY.vocab_size, (1, 256), device=gpu)
+    with torch.no_grad():
+        a = m(ids)
+        old = _lib.lib().hbq_set_generic_only(1)
+        try:
+            b = m(ids)
+        finally:
+            _lib.lib().hbq_set_generic_only(old)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_nonfinite_raises_after_forward_cpu():
+    m = LlamaForCausalLM(TINY).random_init_()
+    with torch.no_grad():
+        m.layers[1].mlp.down_proj.weight.fill_(float("inf"))
+    with pytest.raises(RuntimeError, match="Non-finite output"):
+        m(torch.randint(0, 1000, (1, 8)))
+
+
+@pytest.mark.gpu
+def test_dedupe_equal_to_separate_quantization(gpu):
+    """Quantizing the shared input once gives the same projections as quantizing per projection."""
+    m = LlamaForCausalLM(TINY).random_init_(seed=5).half().to(gpu)
+    p = PTQ(hbq_cfg(), m)
+    p.inject_quantizers()
+    a = m.layers[0].self_attn
+    x = torch.randn(1, 64, TINY.hidden_size, device=gpu).half()
+    with torch.no_grad():
+        sep = [a.q_proj(x), a.k_proj(x), a.v_proj(x)]
+        xq = a.q_proj.aq(x)
+        shared = [a.q_proj.forward_quantized(xq), a.k_proj.forward_quantized(xq), a.v_proj.forward_quantized(xq)]
+    for u, w in zip(sep, shared):
+        assert torch.equal(u.view(torch.int16), w.view(torch.int16))
