@@ -135,24 +135,46 @@ def mx_launcher(x, cfg, codes=True):
 
 
 GEMM_CASES = [
-    # (name, M, K, N, op, group_k, group_n, B layout): "nk" = W[N, K] as FP16AccumMatMul passes it,
-    # "kn" = B[K, N] as the blockquant_ext ops take it
-    ("cfg2_gateup_mxint8_nk", 4096, 4096, 14336, "mxint8", 128, 32, "nk"),
-    ("cfg2_gateup_mxint8_kn", 4096, 4096, 14336, "mxint8", 128, 32, "kn"),
-    ("cfg2_gateup_grouped_nk", 4096, 4096, 14336, "grouped", 128, 0, "nk"),
-    ("cfg2_down_grouped_nk", 4096, 14336, 4096, "grouped", 128, 0, "nk"),
-    ("cfg3_mxint8_nk", 8192, 4096, 4096, "mxint8", 128, 32, "nk"),
+    # (name, M, K, N, op, group_k, group_n, B layout, operand formats): "nk" = W[N, K] as
+    # FP16AccumMatMul passes it, "kn" = B[K, N] as the blockquant_ext ops take it.  Operands are
+    # fake-quantized first (outside the timed region) as the configs prescribe: configs[2] HBQ-E
+    # W4/A5, configs[3] HBQ-E (hbq_e_psum_quant.yaml) and NVFP4 (nvfp4_psum_quant.yaml).
+    ("cfg3_hbqe_mxint8_nk", 8192, 4096, 4096, "mxint8", 128, 32, "nk", "hbq_e"),
+    ("cfg3_nvfp4_mxint8_nk", 8192, 4096, 4096, "mxint8", 128, 32, "nk", "nvfp4"),
+    ("cfg2_gateup_mxint8_nk", 4096, 4096, 14336, "mxint8", 128, 32, "nk", "hbq_e"),
+    ("cfg2_gateup_mxint8_kn", 4096, 4096, 14336, "mxint8", 128, 32, "kn", "hbq_e"),
+    ("cfg2_gateup_grouped_nk", 4096, 4096, 14336, "grouped", 128, 0, "nk", "hbq_e"),
+    ("cfg2_down_grouped_nk", 4096, 14336, 4096, "grouped", 128, 0, "nk", "hbq_e"),
 ]
+
+
+def gemm_operands(dev, M, K, N, fmt, seed):
+    """fp16 activations N(0, 1) with 8 outlier channels x50 and weights N(0, 0.02), fake-quantized
+    with the config's activation / weight quantizers (HBQ-E: act E2M2 SIG-1, wgt E2M1 Mix, l2 block
+    32; NVFP4: E2M1, block 16, E5M3 scale)."""
+    from hbq_amd.quantizer import HBQQuantizer, MXFPQuantizer
+    g = torch.Generator(device=dev).manual_seed(seed)
+    A = torch.randn(M, K, device=dev, generator=g)
+    oc = torch.randperm(K, device=dev, generator=g)[:8]
+    A[:, oc] *= 50.0
+    A = A.half()
+    W = (torch.randn(N, K, device=dev, generator=g) * 0.02).half()
+    if fmt == "hbq_e":
+        aq = HBQQuantizer(block_size=128, ebit=2, mbit=2, sc_ebit=5, sc_mbit=3, l2_block_size=32, l2_sc_bit=2,
+                          l2_scheme="SIG-1")
+        wq = HBQQuantizer(block_size=128, ebit=2, mbit=1, sc_ebit=5, sc_mbit=3, l2_block_size=32, l2_sc_bit=2,
+                          l2_scheme="Mix")
+    else:
+        aq = wq = MXFPQuantizer(block_size=16, ebit=2, mbit=1, sc_ebit=5, sc_mbit=3)
+    return aq.q(A), wq.q(W)
 
 
 def gemm_extra(dev, cases=GEMM_CASES, iters=10):
     """TFLOP/s (2MNK / kernel time) of the block-quant GEMMs at the configs[2..3] shapes."""
     from hbq_amd import blockquant_ext as ext
     out = {}
-    g = torch.Generator(device=dev).manual_seed(3)
-    for name, M, K, N, op, gk, gn, lay in cases:
-        A = torch.randn(M, K, device=dev, generator=g).half()
-        B = (torch.randn(N, K, device=dev, generator=g) * 0.02).half()
+    for ci, (name, M, K, N, op, gk, gn, lay, fmt) in enumerate(cases):
+        A, B = gemm_operands(dev, M, K, N, fmt, seed=3 + ci)
         if lay == "kn":
             B = B.t().contiguous()
         nk = lay == "nk"
@@ -160,7 +182,7 @@ def gemm_extra(dev, cases=GEMM_CASES, iters=10):
             fn = lambda: ext.gemm_blockquant_mxint8(A, B, gk, gn, b_is_nk=nk)
         else:
             fn = lambda: ext.gemm_fp16_grouped_accum(A, B, gk, b_is_nk=nk)
-        for _ in range(5 if name == cases[0][0] else 2):   # the first case also brings the clocks up
+        for _ in range(5 if ci == 0 else 2):   # the first case also brings the clocks up
             fn()
         t = HipTimer().run(fn, iters)
         tf = 2.0 * M * N * K / t / 1e12
@@ -168,6 +190,29 @@ def gemm_extra(dev, cases=GEMM_CASES, iters=10):
         out[f"{name}_frac"] = round(tf / FP16_PEAK_TFLOPS, 4)
         out[f"{name}_ms"] = round(t * 1e3, 3)
         del A, B
+    return out
+
+
+def config0_extra(dev, iters=20):
+    """q_proj-shaped linear, HBQ-A W4/A5 then an fp32-accumulation matmul (W 4096x4096
+    N(0, 0.02), X 2048x4096 N(0, 1) with 8 outlier channels x50, fp16)."""
+    from hbq_amd import blockquant_ext as ext
+    from hbq_amd.quantizer import HBQQuantizer
+    g = torch.Generator(device=dev).manual_seed(1000)
+    W = (torch.randn(4096, 4096, device=dev, generator=g) * 0.02).half()
+    X = torch.randn(2048, 4096, device=dev, generator=g)
+    X[:, torch.randperm(4096, device=dev, generator=g)[:8]] *= 50.0
+    X = X.half()
+    wq = HBQQuantizer(128, 2, 1, 5, 3, 8, 2, "Mix")
+    aq = HBQQuantizer(128, 2, 2, 5, 3, 8, 2, "SIG-1")
+    steps = {"cfg0_wgt_quant_us": lambda: wq.q(W), "cfg0_act_quant_us": lambda: aq.q(X)}
+    Wq, Xq = wq.q(W), aq.q(X)
+    steps["cfg0_gemm_us"] = lambda: ext.gemm_fp32_accum_nk(Xq, Wq)
+    out = {}
+    for name, fn in steps.items():
+        for _ in range(3):
+            fn()
+        out[name] = round(HipTimer().run(fn, iters) * 1e6, 1)
     return out
 
 
@@ -190,6 +235,7 @@ def prefill_extra(dev, T=2048, iters=3):
     """one prefill of T tokens through Llama-3-8B (32 layers, random N(0, 0.02)
     weights, fp16) with the HBQ-A + KV quantization points; weights quantized once beforehand."""
     from hbq_amd.llama import LlamaConfig, LlamaForCausalLM
+    from hbq_amd.ops import use_hip_fp32_gemm
     from hbq_amd.ptq import PTQ
     cfg = LlamaConfig()
     with torch.device(dev):
@@ -197,6 +243,7 @@ def prefill_extra(dev, T=2048, iters=3):
     m.random_init_(seed=4)
     p = PTQ(HBQ_A_KV, m)
     p.inject_quantizers()
+    use_hip_fp32_gemm(m)          # the seven linears of every layer on the HIP GEMM (fp32 accumulation)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     p.static_quant_wgt()
@@ -321,6 +368,7 @@ def main():
                 s4()
             t = HipTimer().run(s4, 100)
             extra[f"{name}_fp16_GBs"] = round(n * mx_bytes_per_elem(c) / t / 1e9, 1)
+        extra.update(config0_extra(dev))
         extra.update(gemm_extra(dev))
         extra.update(prefill_extra(dev))
     # device-to-device copy of the same tensor: the measured bandwidth ceiling, and the

@@ -269,6 +269,16 @@ int launch_tile256(int mode, int gn, const void* A, const void* B, void* C, floa
     // 32-bit element offsets inside the kernel
     if ((int64_t)M * K >= (1ll << 31) || (int64_t)N * K >= (1ll << 31)) return 0;
     if (mode == kFp32) gk = K;
+    // fewer 256x256 tiles than compute units would leave most of the chip idle: the
+    // 128x128 kernel fills it better
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+            cus = n;
+    }
+    if ((int64_t)((M + TM - 1) / TM) * ((N + TN - 1) / TN) < cus) return 0;
     switch (mode) {
         case kGrouped: launch<kGrouped, 4>(A, B, C, P, M, N, K, gk, st); return 1;
         case kFp32: launch<kFp32, 4>(A, B, C, P, M, N, K, gk, st); return 1;

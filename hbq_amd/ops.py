@@ -42,3 +42,37 @@ class FP16AccumMatMul(nn.Module):
         if bias is not None:
             out2d = out2d + bias
         return out2d.view(*orig_shape[:-1], -1)
+
+
+class FP32AccumMatMul(nn.Module):
+    """fp32-accumulation matmul on the HIP GEMM (one fp16 rounding at the end).
+
+    No counterpart in src/ops.py: the reference leaves fp32 accumulation to
+    F.linear (cuBLAS).  This operator puts those linears on the same MFMA kernel as
+    the other accumulation modes (x [.., K] fp16 against W [N, K], bias added in
+    fp16); the fp32 sum order inside a K range differs from any library's, as it
+    does between libraries."""
+
+    def forward(self, x, w, bias=None) -> torch.Tensor:
+        orig_shape = x.shape
+        x2d = x.reshape(-1, x.shape[-1])
+        if x2d.dtype != torch.float16:
+            x2d = x2d.half()
+        w16 = w if w.dtype == torch.float16 else w.half()
+        out2d = ext.gemm_fp32_accum_nk(x2d, w16)
+        if bias is not None:
+            out2d = out2d + bias
+        return out2d.view(*orig_shape[:-1], -1)
+
+
+def use_hip_fp32_gemm(model):
+    """Route every fp32-accumulation _QBaseLinear (ops None) of a model's decoder layers
+    through FP32AccumMatMul."""
+    from .module import _QBaseLinear
+    n = 0
+    for layer in [m for _, m in model.named_modules() if hasattr(m, "self_attn") and hasattr(m, "mlp")]:
+        for mod in layer.modules():
+            if isinstance(mod, _QBaseLinear) and mod.ops is None:
+                mod.ops = FP32AccumMatMul()
+                n += 1
+    return n

@@ -114,3 +114,22 @@ def test_dedupe_equal_to_separate_quantization(gpu):
         shared = [a.q_proj.forward_quantized(xq), a.k_proj.forward_quantized(xq), a.v_proj.forward_quantized(xq)]
     for u, w in zip(sep, shared):
         assert torch.equal(u.view(torch.int16), w.view(torch.int16))
+
+
+@pytest.mark.gpu
+def test_hip_fp32_gemm_linears(gpu):
+    """The prefill with the linears on the HIP fp32-accumulation GEMM stays close to F.linear
+    (same quantized operands; only the fp32 summation order differs)."""
+    from hbq_amd.ops import use_hip_fp32_gemm
+    m = LlamaForCausalLM(TINY).random_init_(seed=6).half().to(gpu)
+    p = PTQ(hbq_cfg(kv=True), m)
+    p.inject_quantizers()
+    p.static_quant_wgt()
+    ids = torch.randint(0, TINY.vocab_size, (1, 128), device=gpu)
+    with torch.no_grad():
+        a = m(ids).float()
+        assert use_hip_fp32_gemm(m) == TINY.num_hidden_layers * 7
+        b = m(ids).float()
+    rel = ((a - b).norm() / a.norm()).item()
+    print(f"hip fp32 gemm vs F.linear: normwise rel {rel:.2e}", flush=True)
+    assert rel < 2e-2
