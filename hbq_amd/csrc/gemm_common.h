@@ -107,17 +107,17 @@ __device__ __forceinline__ void sub_to_hi(h2_t& h, float t, float M) {
 // Fold the 16 fp32 partials of one 32x32 block into the fp16 accumulators H
 // (8 packed pairs; pair p holds registers 2p and 2p + 1, adjacent columns).
 //
-// mxint8: for a group max mx that is finite and nonzero, s = 2^(e - 6) with
-// e = ilogb mx, |P| / s < 128, and rne(P / s) * s = (P + M) - M with
-// M = 1.5 * 2^(e + 17): the add rounds P to the nearest (even) multiple of
+// mxint8: with the group max mx normal (or zero, where the scale is 1),
+// s = 2^(ilogb(mx) - 6), |P| / s < 128, and rne(P / s) * s = (P + M) - M with
+// M = 1.5 * 2^23 * s: the add rounds P to the nearest (even) multiple of
 // ulp(M) = s and the subtraction is exact.  (fp16 products bound |P| by 2^39
-// and nonzero |P| below by 2^-48, so M stays a normal fp32.)  NaN partials stay
-// NaN.  The subtraction and the rounding to fp16 share one v_fma_mix.
-// Only a group whose max lies in the top 1/128 of its binade can round to
-// +-128 s, which the clamp turns into +-127 s = +-128 s * 127/128; such
-// groups, all-zero groups (s = 1), groups with an infinite max (every output
-// NaN, as P / inf * inf) and maxima outside the normal range take a second,
-// rarely used branch.
+// and nonzero |P| below by 2^-48.)  The subtraction and the rounding to fp16
+// share one v_fma_mix.  The clamp of rne(P / s) to +-127 happens on the fp16
+// values: R16 is monotone and only +-128 s exceeds 127 s, so clamping R16(q)
+// to +-R16(127 s) gives R16(clamp(q)); v_pk_minimum3/maximum3 propagate NaN, as
+// the reference does for a NaN partial.  A group with an infinite max (every
+// output NaN, as P / inf * inf) or a max outside the normal range above takes
+// the exact scalar formula.
 template <int MODE, int GN>
 __device__ __forceinline__ void fold_block(const f16v& acc, h2_t* H) {
     if constexpr (MODE == kGrouped) {
@@ -136,14 +136,17 @@ __device__ __forceinline__ void fold_block(const f16v& acc, h2_t* H) {
             if constexpr (GN >= 8) mx = xlane32_max(mx);
             mxg[g] = mx;
             const uint32_t mb = __builtin_bit_cast(uint32_t, mx);
-            special = special || (mb - 0x00800000u) >= (0x76000000u - 0x00800000u) || (mb & 0x7f0000u) == 0x7f0000u;
+            special = special || (mb != 0u && (mb - (27u << 23)) >= ((237u - 27u) << 23));
         }
         if constexpr (MODE == kInt8) {
             if (!special) {
 #pragma unroll
                 for (int g = 0; g < NG; ++g) {
-                    const float M = __builtin_bit_cast(
-                        float, (__builtin_bit_cast(uint32_t, mxg[g]) & 0x7f800000u) + (17u << 23) + 0x400000u);
+                    const uint32_t mb = __builtin_bit_cast(uint32_t, mxg[g]);
+                    const uint32_t sb = mb != 0u ? (mb & 0x7f800000u) - (6u << 23) : 0x3f800000u;   // s
+                    const float M = __builtin_bit_cast(float, sb + (23u << 23) + 0x400000u);       // 1.5 * 2^23 * s
+                    const _Float16 c = (_Float16)(127.0f * __builtin_bit_cast(float, sb));
+                    const h2_t hi = (h2_t){c, c}, lo = -hi;
 #pragma unroll
                     for (int r = g * RPG; r < (g + 1) * RPG; r += 2) {
                         float t0 = acc[r] + M, t1 = acc[r + 1] + M;
@@ -151,6 +154,7 @@ __device__ __forceinline__ void fold_block(const f16v& acc, h2_t* H) {
                         h2_t q;
                         sub_to_lo(q, t0, M);
                         sub_to_hi(q, t1, M);
+                        q = __builtin_elementwise_maximum(__builtin_elementwise_minimum(q, hi), lo);
                         H[r / 2] = H[r / 2] + q;
                     }
                 }
@@ -158,18 +162,9 @@ __device__ __forceinline__ void fold_block(const f16v& acc, h2_t* H) {
                 float q[16];
 #pragma unroll
                 for (int g = 0; g < NG; ++g) {
-                    const float mx = mxg[g];
-                    const float s = psum_scale(mx, 6);
-                    const float M = s * 12582912.f;   // 1.5 * 2^23 * s
-                    const float c128 = 128.f * s;
+                    const float s = psum_scale(mxg[g], 6);
 #pragma unroll
-                    for (int r = g * RPG; r < (g + 1) * RPG; ++r) {
-                        float t = acc[r] + M;
-                        asm("" : "+v"(t));
-                        t = t - M;
-                        t = fabsf(t) == c128 ? t * 0.9921875f : t;
-                        q[r] = mx == __builtin_inff() ? __builtin_nanf("") : t;
-                    }
+                    for (int r = g * RPG; r < (g + 1) * RPG; ++r) q[r] = int8_qdq(acc[r], s, 1.f / s);
                 }
 #pragma unroll
                 for (int p = 0; p < 8; ++p) H[p] = H[p] + cvt2(q[2 * p], q[2 * p + 1]);
