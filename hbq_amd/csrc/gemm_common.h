@@ -95,29 +95,38 @@ __device__ __forceinline__ float xlane32_max(float v) {
     return fmaxf(v, fmaxf(a, b));
 }
 
-// R16(t - M) written to the low or high half of h, in one v_fma_mix (t * 1 - M
-// with a single rounding of the exact difference)
-__device__ __forceinline__ void sub_to_lo(h2_t& h, float t, float M) {
-    asm("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,0]" : "+v"(h) : "v"(t), "v"(M));
+// R16(t0 - M) and R16(t1 - M) packed in one register, each by one v_fma_mix
+// (t * 1 - M with a single rounding of the exact difference).  The first
+// instruction writes only the low half, the second only the high half, so the
+// register needs no prior value.
+__device__ __forceinline__ h2_t sub_pair(float t0, float t1, float M) {
+    h2_t h;
+    asm("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,0]" : "=v"(h) : "v"(t0), "v"(M));
+    asm("v_fma_mixhi_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,0]" : "+v"(h) : "v"(t1), "v"(M));
+    return h;
 }
-__device__ __forceinline__ void sub_to_hi(h2_t& h, float t, float M) {
-    asm("v_fma_mixhi_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,0]" : "+v"(h) : "v"(t), "v"(M));
-}
+
+__device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
 
 // Fold the 16 fp32 partials of one 32x32 block into the fp16 accumulators H
 // (8 packed pairs; pair p holds registers 2p and 2p + 1, adjacent columns).
 //
-// mxint8: with the group max mx normal (or zero, where the scale is 1),
-// s = 2^(ilogb(mx) - 6), |P| / s < 128, and rne(P / s) * s = (P + M) - M with
-// M = 1.5 * 2^23 * s: the add rounds P to the nearest (even) multiple of
-// ulp(M) = s and the subtraction is exact.  (fp16 products bound |P| by 2^39
-// and nonzero |P| below by 2^-48.)  The subtraction and the rounding to fp16
-// share one v_fma_mix.  The clamp of rne(P / s) to +-127 happens on the fp16
-// values: R16 is monotone and only +-128 s exceeds 127 s, so clamping R16(q)
-// to +-R16(127 s) gives R16(clamp(q)); v_pk_minimum3/maximum3 propagate NaN, as
-// the reference does for a NaN partial.  A group with an infinite max (every
-// output NaN, as P / inf * inf) or a max outside the normal range above takes
-// the exact scalar formula.
+// mxint8: with the group max mx normal, s = 2^(ilogb(mx) - 6), |P| / s < 128,
+// and rne(P / s) * s = (P + M) - M with M = 1.5 * 2^23 * s: the add rounds P
+// to the nearest (even) multiple of ulp(M) = s and the subtraction is exact.
+// (fp16 products bound |P| by 2^39 and nonzero |P| below by 2^-48.)  The
+// subtraction and the rounding to fp16 share one v_fma_mix.  NaN partials stay
+// NaN, as in the reference.  Only a group whose max has a mantissa of at least
+// 1 + 127/128 (mx / s >= 127.5) can round to +-128 s; when a lane of the wave
+// holds such a group the block also clamps, on the fp16 values: R16 is
+// monotone and only +-128 s exceeds 127 s, so clamping R16(q) to +-R16(127 s)
+// gives R16(clamp(q)), and v_pk_minimum3/maximum3 propagate NaN.  An all-zero
+// group (mx = 0) gets M = 1.5 * 2^-110 from the same bit arithmetic, which
+// turns every +-0 into +0 (the sign of a zero addend cannot change an
+// accumulator that starts at +0 and only adds fp16 values).  When a lane holds
+// a group with an infinite max (every output NaN, as P / inf * inf) or a
+// nonzero max outside [2^-100, 2^110), the whole wave takes the exact formula.
+// The branches depend on wave-wide ballots, so they are scalar branches.
 template <int MODE, int GN>
 __device__ __forceinline__ void fold_block(const f16v& acc, h2_t* H) {
     if constexpr (MODE == kGrouped) {
@@ -127,7 +136,7 @@ __device__ __forceinline__ void fold_block(const f16v& acc, h2_t* H) {
         constexpr int RPG = GN >= 8 ? GN / 2 : 4;     // registers of one column group in this lane
         constexpr int NG = 16 / RPG;
         float mxg[NG];
-        bool special = false;
+        bool special = false, top = false;
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
             float mx = 0.f;
@@ -135,27 +144,37 @@ __device__ __forceinline__ void fold_block(const f16v& acc, h2_t* H) {
             for (int r = g * RPG; r < (g + 1) * RPG; ++r) mx = fmaxf(mx, fabsf(acc[r]));
             if constexpr (GN >= 8) mx = xlane32_max(mx);
             mxg[g] = mx;
-            const uint32_t mb = __builtin_bit_cast(uint32_t, mx);
-            special = special || (mb != 0u && (mb - (27u << 23)) >= ((237u - 27u) << 23));
+            special |= (mx >= 0x1p110f) | ((mx < 0x1p-100f) & (mx != 0.f));
+            top |= (__builtin_bit_cast(uint32_t, mx) & 0x7fffffu) >= 0x7f0000u;
         }
         if constexpr (MODE == kInt8) {
-            if (!special) {
+            if (__builtin_expect(!wave_any(special), 1)) {
+                float Mg[NG];
 #pragma unroll
-                for (int g = 0; g < NG; ++g) {
-                    const uint32_t mb = __builtin_bit_cast(uint32_t, mxg[g]);
-                    const uint32_t sb = mb != 0u ? (mb & 0x7f800000u) - (6u << 23) : 0x3f800000u;   // s
-                    const float M = __builtin_bit_cast(float, sb + (23u << 23) + 0x400000u);       // 1.5 * 2^23 * s
-                    const _Float16 c = (_Float16)(127.0f * __builtin_bit_cast(float, sb));
-                    const h2_t hi = (h2_t){c, c}, lo = -hi;
+                for (int g = 0; g < NG; ++g)   // 1.5 * 2^23 * 2^(ilogb(mx) - 6)
+                    Mg[g] = __builtin_bit_cast(
+                        float, (__builtin_bit_cast(uint32_t, mxg[g]) & 0x7f800000u) + (17u << 23) + 0x400000u);
+                if (__builtin_expect(!wave_any(top), 1)) {
 #pragma unroll
-                    for (int r = g * RPG; r < (g + 1) * RPG; r += 2) {
-                        float t0 = acc[r] + M, t1 = acc[r + 1] + M;
-                        asm("" : "+v"(t0), "+v"(t1));
-                        h2_t q;
-                        sub_to_lo(q, t0, M);
-                        sub_to_hi(q, t1, M);
-                        q = __builtin_elementwise_maximum(__builtin_elementwise_minimum(q, hi), lo);
-                        H[r / 2] = H[r / 2] + q;
+                    for (int g = 0; g < NG; ++g)
+#pragma unroll
+                        for (int r = g * RPG; r < (g + 1) * RPG; r += 2) {
+                            const float t0 = acc[r] + Mg[g], t1 = acc[r + 1] + Mg[g];
+                            H[r / 2] = H[r / 2] + sub_pair(t0, t1, Mg[g]);
+                        }
+                } else {
+#pragma unroll
+                    for (int g = 0; g < NG; ++g) {
+                        const uint32_t mb = __builtin_bit_cast(uint32_t, mxg[g]);
+                        const float s = mb != 0u ? __builtin_bit_cast(float, (mb & 0x7f800000u) - (6u << 23)) : 1.0f;
+                        const _Float16 c = (_Float16)(127.0f * s);
+                        const h2_t hi = (h2_t){c, c}, lo = -hi;
+#pragma unroll
+                        for (int r = g * RPG; r < (g + 1) * RPG; r += 2) {
+                            const float t0 = acc[r] + Mg[g], t1 = acc[r + 1] + Mg[g];
+                            const h2_t q = sub_pair(t0, t1, Mg[g]);
+                            H[r / 2] = H[r / 2] + __builtin_elementwise_maximum(__builtin_elementwise_minimum(q, hi), lo);
+                        }
                     }
                 }
             } else {
