@@ -68,6 +68,14 @@ __device__ __forceinline__ uint32_t bits_of(float v) {
     return (uint32_t)T::store(v);
 }
 
+// ordering key of a value already representable in T: its bit pattern shifted
+// left by 16 for bf16 (the float's own bits, low half zero), as is for fp16
+template <class T>
+__device__ __forceinline__ uint32_t key_of(float v) {
+    if (T::dt == kBF16) return f2bits(v);
+    return (uint32_t)T::store(v);
+}
+
 template <class T>
 __device__ __forceinline__ float from_bits(uint32_t b) {
     return T::load((typename T::storage)b);
@@ -246,35 +254,31 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
             for (int i = 0; i < 8; ++i) xp[i] = __builtin_bit_cast(h2_t, w[i] & 0x7fff7fffu);
         }
         uint32_t ent[S][kV];
-        uint32_t tb[S][kV];      // bit patterns of t = R_T(|x| / l1): non-negative, so ordered as integers
+        // keys of t = R_T(|x| / l1): T's bit pattern shifted left by KSH (bf16: the
+        // float bits of t, as BF16::round leaves them); non-negative, so ordered as integers
+        constexpr int KSH = T::dt == kBF16 ? 16 : 0;
+        uint32_t tb[S][kV];
         int jsel[S][NSUBL];
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             const float rl1 = 1.0f / l1[s];
             float qmin = xa[0] * rl1;
 #pragma unroll
-            for (int i = 0; i < kV; i += 2) {
-                const float q0 = xa[i] * rl1, q1 = xa[i + 1] * rl1;
-                qmin = fminf(qmin, fminf(q0, q1));
-                if constexpr (T::dt == kBF16) {
-                    const uint32_t r = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){q0, q1}, bf16x2_t));
-                    tb[s][i] = r & 0xffffu;
-                    tb[s][i + 1] = r >> 16;
-                } else {
-                    tb[s][i] = bits_of<T>(T::round(q0));
-                    tb[s][i + 1] = bits_of<T>(T::round(q1));
-                }
+            for (int i = 0; i < kV; ++i) {
+                const float q = xa[i] * rl1;
+                qmin = fminf(qmin, q);
+                tb[s][i] = key_of<T>(T::round(q));
             }
             if (qmin < tiny) {   // quotients in T's subnormal range can be exact ties: divide
 #pragma unroll
                 for (int i = 0; i < kV; ++i)
-                    if (xa[i] * rl1 < tiny) tb[s][i] = bits_of<T>(T::round(xa[i] / l1[s]));
+                    if (xa[i] * rl1 < tiny) tb[s][i] = key_of<T>(T::round(xa[i] / l1[s]));
             }
 #pragma unroll
             for (int i = 0; i < kV; ++i) {
-                int k = (int)tb[s][i] - (int)p.lo_bits + 1;
-                k = k < 0 ? 0 : (k > p.n + 1 ? p.n + 1 : k);
-                ent[s][i] = lut[s * per + k];
+                int k;   // clamp to [-1, n] in one v_med3_i32; word k + 1 (0 and n + 1 are the sentinels)
+                asm("v_med3_i32 %0, %1, -1, %2" : "=v"(k) : "v"((int)(tb[s][i] >> KSH) - (int)p.lo_bits), "s"(p.n));
+                ent[s][i] = lut[s * per + k + 1];
             }
             float best[NSUBL];
 #pragma unroll
@@ -283,7 +287,8 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
                 const char* rowb = drow0 + ((s * kFastJ + j) * bpw) * ROW * sizeof(DT);
 #pragma unroll
                 for (int sb = 0; sb < NSUBL; ++sb) {
-                    float acc = 0.f;
+                    // the squares are >= +0, so starting from the first one equals torch's 0 + ...
+                    float acc;
 #pragma unroll
                     for (int i = sb * SUBN; i < (sb + 1) * SUBN; i += 2) {
                         const DT d0 = *reinterpret_cast<const DT*>(rowb + ((ent[s][i] >> (8 * j)) & 0xffu));
@@ -293,13 +298,13 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
                             const h2_t e = xp[i / 2] - (h2_t){d0, d1};
                             h2_t q = e * e;
                             asm("" : "+v"(q));
-                            acc += (float)q.x;
+                            acc = i == sb * SUBN ? (float)q.x : acc + (float)q.x;
                             acc += (float)q.y;
                         } else {
                             float e0, e1, q0, q1;
                             round2<T>(xa[i] - (float)d0, xa[i + 1] - (float)d1, e0, e1);
                             round2<T>(e0 * e0, e1 * e1, q0, q1);
-                            acc += q0;
+                            acc = i == sb * SUBN ? q0 : acc + q0;
                             acc += q1;
                         }
                     }
@@ -357,7 +362,7 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
             float zz = z[s][0];
 #pragma unroll
             for (int jj = 1; jj < kFastJ; ++jj) zz = j == jj ? z[s][jj] : zz;
-            zsel[sb] = bits_of<T>(zz);
+            zsel[sb] = key_of<T>(zz);
         }
 #pragma unroll
         for (int i = 0; i < kV; ++i) {

@@ -35,6 +35,9 @@ struct F16 {
     __device__ __forceinline__ static float round(float v) { return load(store(v)); }
 };
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
 struct BF16 {
     using storage = uint16_t;
     static constexpr DType dt = kBF16;
@@ -42,7 +45,11 @@ struct BF16 {
     __device__ __forceinline__ static storage store(float v) {
         return __builtin_bit_cast(uint16_t, (__bf16)v);   // v_cvt_pk_bf16_f32: RNE, subnormals kept
     }
-    __device__ __forceinline__ static float round(float v) { return load(store(v)); }
+    // v_cvt_pk_bf16_f32 d, 0, v: the high half holds R(v), the low half R(0) = 0,
+    // so d is already the float R(v) -- one instruction, no unpacking
+    __device__ __forceinline__ static float round(float v) {
+        return __builtin_bit_cast(float, __builtin_convertvector((f32x2_t){0.0f, v}, bf16x2_t));
+    }
 };
 
 struct F32 {
@@ -53,20 +60,12 @@ struct F32 {
     __device__ __forceinline__ static float round(float v) { return v; }
 };
 
-// Round two floats to T at once (one v_cvt_pk_bf16_f32 for bf16).
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
+// Round two floats to T.  (For bf16 one v_cvt_pk_bf16_f32 per value beats one
+// per pair: the pair would need two instructions to unpack.)
 template <class T>
 __device__ __forceinline__ void round2(float a, float b, float& ra, float& rb) {
-    if constexpr (T::dt == kBF16) {
-        const bf16x2_t r = __builtin_convertvector((f32x2_t){a, b}, bf16x2_t);
-        const uint32_t u = __builtin_bit_cast(uint32_t, r);
-        ra = bits2f(u << 16);
-        rb = bits2f(u & 0xffff0000u);
-    } else {
-        ra = T::round(a);
-        rb = T::round(b);
-    }
+    ra = T::round(a);
+    rb = T::round(b);
 }
 
 // ---- binade exponent and the rounded-log2 exponent ------------------------

@@ -178,7 +178,9 @@ struct HbqParams {
     ScaleFmt sf;                 // E5M3 L1 scale format
 };
 
-__device__ __forceinline__ bool better(float v, float best) { return (v != v) ? (best == best) : (v < best); }
+// v replaces best (torch.argmin order: NaN is the smallest, the first minimum wins):
+// v < best, or v NaN and best not.  !(v >= best) is v < best or either NaN.
+__device__ __forceinline__ bool better(float v, float best) { return !(v >= best) & (best == best); }
 
 // torch's fp32 order for the block error of one scheme (four interleaved
 // cascades over the 128.. elements, combined left to right), computed by the
