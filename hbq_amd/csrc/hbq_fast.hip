@@ -52,6 +52,7 @@ struct FastParams {
     uint32_t lo_bits;          // T bit pattern of 2^lo
     float l2[kFastJ][2];       // L2 factors
     float em[2];
+    float rem[2];              // R32(1 / em): R_T(amax * rem) equals R_T(amax / em) wherever the clamp below keeps it
     int use_ceil;
 };
 
@@ -207,14 +208,12 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
 #pragma unroll
             for (int i = 0; i < 8; ++i) w[i] = 0u;
         }
-        uint32_t m2 = 0;
+        // packed 16-bit maxima (v_pk_max_u16) of the sign-cleared patterns, then the two halves
+        typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
+        u16x2_t mp = __builtin_bit_cast(u16x2_t, w[0] & 0x7fff7fffu);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t a = w[i] & 0x7fff7fffu;
-            const uint32_t lo = a & 0xffffu, hi = a >> 16;
-            const uint32_t mx = lo > hi ? lo : hi;
-            m2 = m2 > mx ? m2 : mx;
-        }
+        for (int i = 1; i < 8; ++i) mp = __builtin_elementwise_max(mp, __builtin_bit_cast(u16x2_t, w[i] & 0x7fff7fffu));
+        uint32_t m2 = mp.x > mp.y ? (uint32_t)mp.x : (uint32_t)mp.y;
         m2 = max8_dpp(m2);
         const float amax = T::load((typename T::storage)m2);
         float xv[kV], xa[kV];
@@ -229,7 +228,9 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
         float l1[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-            float sc = T::round(amax / p.em[s]);
+            // R_T(amax * R32(1/em)) = R_T(amax / em) for quotients in T's normal range;
+            // below it both clamp to 2^-14 (exhaustive CPU check over every T value)
+            float sc = T::round(amax * p.rem[s]);
             sc = sc < 6.103515625e-05f ? 6.103515625e-05f : (sc > 61440.f ? 61440.f : sc);
             l1[s] = sc != sc ? sc : e5m3_scale<T>(sc, p.use_ceil);
         }
@@ -520,6 +521,8 @@ int hbq_fast_try(const void* x, void* y, void* l1, void* l2i, void* sch, void* c
         for (int s = 0; s < 2; ++s) p.l2[j][s] = j < hp.J ? hp.l2[j][s] : 1.f;
     p.em[0] = hp.em[0];
     p.em[1] = hp.em[S - 1];
+    p.rem[0] = 1.0f / p.em[0];
+    p.rem[1] = 1.0f / p.em[1];
     p.use_ceil = hp.sf.use_ceil;
     // the kernel quantizes the L1 scale to E5M3 without subnormals
     if (hp.sf.allow_sub || hp.sf.emax != 15.f || hp.sf.mshift != 8.f || hp.sf.emin != -14.f) return 0;

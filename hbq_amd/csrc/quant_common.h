@@ -42,7 +42,13 @@ __device__ __forceinline__ void store16(typename T::storage* __restrict__ p, con
     if constexpr (sizeof(typename T::storage) == 2) {
         uint32_t w[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) w[i] = (uint32_t)T::store(v[2 * i]) | ((uint32_t)T::store(v[2 * i + 1]) << 16);
+        for (int i = 0; i < 8; ++i) {
+            if constexpr (T::dt == kBF16) {   // one v_cvt_pk_bf16_f32 per pair
+                w[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){v[2 * i], v[2 * i + 1]}, bf16x2_t));
+            } else {
+                w[i] = (uint32_t)T::store(v[2 * i]) | ((uint32_t)T::store(v[2 * i + 1]) << 16);
+            }
+        }
         u32x4* q = reinterpret_cast<u32x4*>(p);
         __builtin_nontemporal_store((u32x4){w[0], w[1], w[2], w[3]}, q);
         __builtin_nontemporal_store((u32x4){w[4], w[5], w[6], w[7]}, q + 1);

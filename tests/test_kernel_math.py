@@ -57,3 +57,30 @@ def test_fp16_double_rounding_innocuous():
             twice = op(a.astype(np.float32), b.astype(np.float32)).astype(np.float16)
         same = (once == twice) | (np.isnan(once) & np.isnan(twice))
         assert same.all(), op
+
+
+def _elem_max_divisors(dt):
+    """em = R_T(ele_max * max_j l2_j) of every configuration the table-driven HBQ kernel takes:
+    E2M1..E2M3 elements, l2_sc_bit 0..2, every L2 scheme (src/quantizer.py:745-770)."""
+    out = set()
+    for ele_max in (6.0, 7.0, 7.5):
+        for sc_bit in (0, 1, 2):
+            J = 1 << sc_bit
+            r = J - 1
+            for m in (2.0 ** r, r + 1, 1 + r / 2, 1 + r / J, 1 + (r + 1) / J, 1 + r / (2 * J), 1 + r / (4 * J)):
+                out.add(float(_round_T(np.array([ele_max * m], np.float64).astype(np.float32), dt)[0]))
+    return sorted(out)
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_elem_max_reciprocal(dt):
+    """The table kernel's L1 scale input R_T(amax * R32(1/em)), clamped to [2^-14, 61440] as the
+    kernel does, equals the reference's R_T(amax / em) clamped, for every non-negative T value amax
+    and every element-max divisor em."""
+    a = _values(dt)
+    a = a[a >= 0]
+    for em in _elem_max_divisors(dt):
+        exact = _round_T((a.astype(np.float64) / em).astype(np.float32), dt)
+        approx = _round_T((a * (np.float32(1.0) / np.float32(em))).astype(np.float32), dt)
+        lo, hi = np.float32(2.0 ** -14), np.float32(61440.0)
+        assert np.array_equal(np.clip(exact, lo, hi), np.clip(approx, lo, hi)), em
