@@ -229,3 +229,31 @@ def test_transpose16(gpu, shape):
     dst = torch.empty((cols, rows), device=gpu, dtype=torch.int16)
     _lib.check(_lib.lib().hbq_transpose16(_lib.ptr(src), _lib.ptr(dst), rows, cols, _lib.stream_of(src)))
     assert torch.equal(dst, src.t())
+
+
+@pytest.mark.parametrize("op,gk,gn", [("fp32", 0, 0), ("grouped", 128, 0), ("mxint8", 128, 32), ("mxint8", 256, 16),
+                                      ("mxint8", 128, 4), ("mxfp8", 128, 32), ("mxfp8", 256, 8)])
+@pytest.mark.parametrize("K", [256, 512])
+def test_large_tile_kernel_bit_identical(gpu, op, gk, gn, K):
+    """At shapes with enough 256x256 tiles to fill the chip (16 x 16 here, the last tile row
+    ragged) W[N,K] runs on the 256x256 kernel, while B[K,N] without the transpose runs on the
+    128x128 kernel that the oracle tests pin: the same bits."""
+    from hbq_amd import blockquant_ext as ext
+    M, N = 4000, 4096
+    print(f"large tiles {op} gk={gk} gn={gn} K={K}", flush=True)
+    A = synth(M, K, 51, "f16").to(gpu)
+    B = synth(K, N, 52, "f16", std=0.02).to(gpu)
+    W = B.t().contiguous()
+    call = {"fp32": lambda b, nk: ext.gemm_fp32_accum(A, b, b_is_nk=nk),
+            "grouped": lambda b, nk: ext.gemm_fp16_grouped_accum(A, b, gk, b_is_nk=nk),
+            "mxint8": lambda b, nk: ext.gemm_blockquant_mxint8(A, b, gk, gn, b_is_nk=nk),
+            "mxfp8": lambda b, nk: ext.gemm_blockquant_mxfp8(A, b, gk, gn, b_is_nk=nk)}[op]
+    old = ext.TRANSPOSE_MIN_MNK
+    try:
+        ext.TRANSPOSE_MIN_MNK = 1 << 62
+        small = call(B, False)
+    finally:
+        ext.TRANSPOSE_MIN_MNK = old
+    big = call(W, True)
+    assert torch.isfinite(small.float()).all()
+    assert torch.equal(small.view(torch.int16), big.view(torch.int16))
