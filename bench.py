@@ -12,7 +12,7 @@ The other formats of configs[1] and the block-quant GEMMs of configs[2..3] are
 measured in the same run and reported under "extra"; the CPU oracle is timed
 on the host cores as the baseline.
 
-Usage:  python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+Usage:  python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick | --quant-only | --gemm-only | --prefill-only]
 """
 import argparse
 import json
@@ -312,6 +312,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only: skip the extra formats, GEMMs and CPU leg")
     ap.add_argument("--gemm-only", action="store_true", help="print only the GEMM measurements")
     ap.add_argument("--prefill-only", action="store_true", help="print only the configs[4] prefill measurement")
+    ap.add_argument("--quant-only", action="store_true", help="headline and the configs[1] formats: skip the "
+                    "configs[0] / GEMM / prefill measurements and the CPU leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the HBQ hot path here has no multi-GPU mode (--gpus {args.gpus} "
@@ -368,9 +370,11 @@ def main():
                 s4()
             t = HipTimer().run(s4, 100)
             extra[f"{name}_fp16_GBs"] = round(n * mx_bytes_per_elem(c) / t / 1e9, 1)
-        extra.update(config0_extra(dev))
-        extra.update(gemm_extra(dev))
-        extra.update(prefill_extra(dev))
+            extra[f"{name}_fp16_frac"] = round(n * mx_bytes_per_elem(c) / t / 1e9 / HBM_PEAK_GBS, 4)
+        if not args.quant_only:
+            extra.update(config0_extra(dev))
+            extra.update(gemm_extra(dev))
+            extra.update(prefill_extra(dev))
     # device-to-device copy of the same tensor: the measured bandwidth ceiling, and the
     # known-size kernel that scales the HBM byte counters
     dst = torch.empty_like(x)
@@ -397,7 +401,7 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic("hbq_a_act_config1")},
         "extra": extra,
     }
-    if not args.quick:
+    if not (args.quick or args.quant_only):
         bits = x_cpu.contiguous().view(torch.int16).numpy().view("uint16")
         out["cpu_baseline"] = cpu_baseline(bits, cfg, bpe, reps=2)
     print(json.dumps(out))

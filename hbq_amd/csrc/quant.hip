@@ -13,6 +13,7 @@
 
 #include "hbq_capi_internal.h"
 #include "hbq_fast.h"
+#include "mx_fast.h"
 #include "quant_common.h"
 #include "hbq_block.h"
 
@@ -21,34 +22,6 @@ namespace hbq {
 // ---------------------------------------------------------------------------
 // MXFP / NVFP  (MXFPQuantizer.get_shared_scale + q, src/quantizer.py:481-539)
 // ---------------------------------------------------------------------------
-struct MxParams {
-    int pot;              // 1: power-of-two scale (sc_mbit == 0), 0: FP scale
-    int use_round;
-    float ele_emax;       // 2^(ebit-1)
-    float sc_emin, sc_emax;
-    float min_normal;     // added to an all-zero block before log2
-    float ele_maxnorm;    // element max normal (FP scale divisor)
-    ScaleFmt sf;          // FP scale format
-    int per_tensor;
-    float tscale;         // per-tensor scale, already rounded to T
-};
-
-template <class T>
-__device__ __forceinline__ float mx_shared_scale(float amax, const MxParams& p) {
-    if (p.pot) {
-        float v = T::round(amax + (amax == 0.f ? p.min_normal : 0.f));
-        float se;
-        if (v != v) se = v;
-        else if (v == __builtin_inff()) se = __builtin_inff();
-        else se = log2_exponent<T>(v, p.use_round);
-        se = T::round(se - p.ele_emax);
-        se = se < p.sc_emin ? p.sc_emin : (se > p.sc_emax ? p.sc_emax : se);
-        if (se != se) return se;
-        return T::round(pow2f((int)se));
-    }
-    return scale_quant<T>(T::round(amax / p.ele_maxnorm), p.sf);
-}
-
 template <class T, int M>
 __global__ __launch_bounds__(kThreads) void mxfp_qdq_kernel(const typename T::storage* __restrict__ x,
                                                             typename T::storage* __restrict__ y,
@@ -295,7 +268,7 @@ static int g_hbq_force_generic = 0;
 
 extern "C" {
 
-// Test hook: 1 routes every HBQ call to the generic kernel (so both kernels can be checked).
+// Test hook: 1 routes every HBQ and MXFP / NVFP call to the generic kernels (so both can be checked).
 int hbq_set_generic_only(int on) {
     int old = g_hbq_force_generic;
     g_hbq_force_generic = on;
@@ -329,6 +302,11 @@ int hbq_mxfp_qdq(const void* x, void* y, void* scales, void* codes, int64_t rows
     p.per_tensor = per_tensor_scale;
     p.tscale = round_host(tensor_scale, dtype);
     hipStream_t st = (hipStream_t)stream;
+    if (!g_hbq_force_generic) {
+        const int fr = hbq_mx_fast_try(x, y, scales, codes, rows, cols, dtype, block_size, mbit, p, st);
+        if (fr < 0) return -fr;
+        if (fr == 1) return hbq_check_launch("hbq_mxfp_qdq");
+    }
     int rc;
     if (dtype == kF16) rc = dispatch_mx_m<F16>(mbit, g, x, y, scales, codes, cols, block_size, p, st);
     else if (dtype == kBF16) rc = dispatch_mx_m<BF16>(mbit, g, x, y, scales, codes, cols, block_size, p, st);

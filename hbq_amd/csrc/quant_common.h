@@ -176,6 +176,35 @@ __device__ __forceinline__ void store_lane(typename T::storage* __restrict__ y, 
 
 constexpr int kMaxJ = 8;
 
+// MXFP / NVFP parameters (MXFPQuantizer, src/quantizer.py:430-511)
+struct MxParams {
+    int pot;              // 1: power-of-two scale (sc_mbit == 0), 0: FP scale
+    int use_round;
+    float ele_emax;       // 2^(ebit-1)
+    float sc_emin, sc_emax;
+    float min_normal;     // added to an all-zero block before log2
+    float ele_maxnorm;    // element max normal (FP scale divisor)
+    ScaleFmt sf;          // FP scale format
+    int per_tensor;
+    float tscale;         // per-tensor scale, already rounded to T
+};
+
+template <class T>
+__device__ __forceinline__ float mx_shared_scale(float amax, const MxParams& p) {
+    if (p.pot) {
+        float v = T::round(amax + (amax == 0.f ? p.min_normal : 0.f));
+        float se;
+        if (v != v) se = v;
+        else if (v == __builtin_inff()) se = __builtin_inff();
+        else se = log2_exponent<T>(v, p.use_round);
+        se = T::round(se - p.ele_emax);
+        se = se < p.sc_emin ? p.sc_emin : (se > p.sc_emax ? p.sc_emax : se);
+        if (se != se) return se;
+        return T::round(pow2f((int)se));
+    }
+    return scale_quant<T>(T::round(amax / p.ele_maxnorm), p.sf);
+}
+
 struct HbqParams {
     int J;                       // number of L2 candidates (2^l2_sc_bit)
     float l2[kMaxJ][2];          // L2 factors per candidate and scheme, in T

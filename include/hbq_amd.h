@@ -53,8 +53,9 @@ const char *hbq_last_error(void);
 /* ABI revision of this header. */
 int hbq_abi_version(void);
 
-/* No reference counterpart: a test hook.  on != 0 routes every hbq_hbq_qdq call
- * to the generic kernel instead of the table-driven one; returns the old setting. */
+/* No reference counterpart: a test hook.  on != 0 routes every hbq_hbq_qdq and
+ * hbq_mxfp_qdq call to the generic kernels instead of the table-driven ones;
+ * returns the old setting. */
 int hbq_set_generic_only(int on);
 
 /*

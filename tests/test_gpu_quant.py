@@ -259,3 +259,31 @@ def test_hbq_table_kernel_equals_generic(gpu, name, dt):
     assert torch.equal(fast.codes[per_byte], gen.codes[per_byte])
     assert mismatches(to_bits(fast.scales), to_bits(gen.scales), dt) == 0
     assert torch.equal(fast.l2_index, gen.l2_index) and torch.equal(fast.scheme, gen.scheme)
+
+
+MXFAST = dict(MXCFG, e2m2_pot=dict(block_size=32, ebit=2, mbit=2, sc_ebit=8, sc_mbit=0),
+              e2m3_fp=dict(block_size=16, ebit=2, mbit=3, sc_ebit=5, sc_mbit=3),
+              e2m5_fp=dict(block_size=32, ebit=2, mbit=5, sc_ebit=4, sc_mbit=3))
+
+
+@pytest.mark.parametrize("name", list(MXFAST))
+def test_mxfp_table_kernel_equals_generic(gpu, name):
+    """The table-driven MXFP / NVFP kernel (fp16, whole blocks) and the generic kernel agree
+    bit for bit on outputs, codes and scales, edge rows (zeros, +-inf, NaN, huge, subnormal,
+    quotients in the fp16 subnormal range) included."""
+    from hbq_amd import _lib
+    print(f"mx fast vs generic {name}", flush=True)
+    x = _edge_rows(synth(512, 4096, 18, "f16"))
+    x[6] = x[6] * 1e-3            # blocks whose quotients reach the fp16 subnormal range
+    x[7, ::3] = 0.0
+    xg = x.to(gpu)
+    q = _mx(MXFAST[name])
+    fast = q.quantize(xg)
+    old = _lib.lib().hbq_set_generic_only(1)
+    try:
+        gen = q.quantize(xg)
+    finally:
+        _lib.lib().hbq_set_generic_only(old)
+    assert mismatches(to_bits(fast.y), to_bits(gen.y), "f16") == 0
+    assert torch.equal(fast.codes, gen.codes)
+    assert mismatches(to_bits(fast.scales), to_bits(gen.scales), "f16") == 0
