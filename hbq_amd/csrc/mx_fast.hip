@@ -29,52 +29,85 @@
 namespace hbq {
 
 constexpr int kMxSlots = 8;
-constexpr int kMxMaxEntries = 10 * 1024 + 2;   // E2M5: binades 2^-7 .. 2^3
+constexpr int kMxMaxWords = 10 * 1024 + 2;   // E2M5: binades 2^-7 .. 2^3, plus 2 sentinels
+constexpr int kMxMagBytes = 256;             // fp16 magnitudes of up to 128 levels
+constexpr int kMxTabBytes = (kMxMagBytes + kMxMaxWords + 15) / 16 * 16;
 
-// per slot: word k + 1 describes u with fp16 bits lo_bits + k; word 0 is below
-// the range (level 0, magnitude 0), word n + 1 at or above it (saturated).
-// Word layout: bits 0-7 the level, bits 16-31 the fp16 bits of its magnitude.
-static __device__ uint32_t g_mx_lut[kMxSlots][kMxMaxEntries];
+// per slot: bytes [0, 256) the fp16 magnitude of every level; from byte 256 the
+// level of each u: byte 256 + k + 1 for u with fp16 bits lo_bits + k, byte 256
+// below the range (level 0), byte 256 + n + 1 at or above it (saturated)
+static __device__ __attribute__((aligned(16))) uint8_t g_mx_tab[kMxSlots][kMxTabBytes];
 static __device__ int g_mx_status[kMxSlots];
+static __device__ int g_mx_bad[kMxSlots];
 
 template <int M>
-__device__ __forceinline__ uint32_t mx_word(float u) {
+__device__ __forceinline__ float mx_level_value(int c) {
+    const int ef = c >> M, mf = c & ((1 << M) - 1);
+    return ef == 0 ? (float)mf * (1.0f / (float)(1 << M)) : (1.0f + (float)mf * (1.0f / (float)(1 << M))) * pow2f(ef - 1);
+}
+
+template <int M>
+__device__ __forceinline__ uint32_t mx_level(float u, float& mag) {
     uint32_t c;
-    const float q = elem_quant<F16, M>(u, c);
-    return (c & ((1u << (M + 2)) - 1u)) | ((uint32_t)F16::store(fabsf(q)) << 16);
+    mag = fabsf(elem_quant<F16, M>(u, c));
+    return c & ((1u << (M + 2)) - 1u);
 }
 
 template <int M>
 __global__ void build_mx_lut_kernel(int slot, int n, uint32_t lo_bits) {
     const int per = n + 2;
+    uint8_t* tab = g_mx_tab[slot];
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < per; i += gridDim.x * blockDim.x) {
-        float u;
+        float u, mag;
         if (i == 0) u = 0.f;
         else if (i == per - 1) u = 65504.f;   // fp16 max: saturated
         else u = F16::load((uint16_t)(lo_bits + (uint32_t)(i - 1)));
-        g_mx_lut[slot][i] = mx_word<M>(u);
+        const uint32_t lv = mx_level<M>(u, mag);
+        tab[kMxMagBytes + i] = (uint8_t)lv;
+        // the table stores one magnitude per level: every u of a level must give it
+        if (F16::store(mag) != F16::store(mx_level_value<M>((int)lv))) atomicMax(&g_mx_bad[slot], 4);
     }
+    const int g = blockIdx.x * blockDim.x + threadIdx.x;
+    if (g < (1 << (M + 2))) reinterpret_cast<uint16_t*>(tab)[g] = F16::store(mx_level_value<M>(g));
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         // the constant ends: the largest value below 2^lo has level 0, 2^hi (the
         // first value above the range) is already saturated
         int status = 0;
-        if ((mx_word<M>(F16::load((uint16_t)(lo_bits - 1u))) & 0xffu) != 0u) status = 1;
-        if (mx_word<M>(F16::load((uint16_t)(lo_bits + (uint32_t)n))) != mx_word<M>(65504.f)) status = 2;
-        if ((mx_word<M>(65504.f) & 0xffu) != (1u << (M + 2)) - 1u) status = 3;
+        float m0, m1, m2;
+        if (mx_level<M>(F16::load((uint16_t)(lo_bits - 1u)), m0) != 0u) status = 1;
+        if (mx_level<M>(F16::load((uint16_t)(lo_bits + (uint32_t)n)), m1) != (1u << (M + 2)) - 1u) status = 2;
+        if (mx_level<M>(65504.f, m2) != (1u << (M + 2)) - 1u || m1 != m2) status = 3;
         g_mx_status[slot] = status;
     }
+}
+
+// R16(|lo half of h| * f) into the low half of the result, one v_fma_mix (a single rounding)
+__device__ __forceinline__ uint32_t mix_lo(uint32_t h, float f) {
+    uint32_t d;
+    asm("v_fma_mixlo_f16 %0, |%1|, %2, 0 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(h), "v"(f));
+    return d;
+}
+// R16(|high half of h| * f) into the high half of d
+__device__ __forceinline__ void mix_hi(uint32_t& d, uint32_t h, float f) {
+    asm("v_fma_mixhi_f16 %0, |%1|, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(d) : "v"(h), "v"(f));
 }
 
 // LPB lanes of 16 elements per block (block 16 or 32), persistent workgroups
 template <int M, int LPB>
 __global__ __launch_bounds__(kThreads) void mx_fast_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
                                                            uint16_t* __restrict__ scales, uint8_t* __restrict__ codes,
-                                                           int64_t nb, int slot, int n, uint32_t lo_bits, MxParams p) {
+                                                           int64_t nb, int slot, int n, uint32_t lo_m1, MxParams p) {
     constexpr int block = kV * LPB;
     constexpr int blocks_per_wg = kThreads / LPB;
-    extern __shared__ uint32_t lut[];
-    for (int i = threadIdx.x; i < n + 2; i += kThreads) lut[i] = g_mx_lut[slot][i];
+    extern __shared__ __attribute__((aligned(16))) uint8_t tab[];
+    {   // copy the table in 16-byte pieces
+        const uint4* src = reinterpret_cast<const uint4*>(g_mx_tab[slot]);
+        uint4* dst = reinterpret_cast<uint4*>(tab);
+        for (int i = threadIdx.x; i < (kMxMagBytes + n + 2 + 15) / 16; i += kThreads) dst[i] = src[i];
+    }
     __syncthreads();
+    const uint16_t* mags = reinterpret_cast<const uint16_t*>(tab);
+    const uint8_t* lvls = tab + kMxMagBytes;   // lvls[k + 1] for u with fp16 bits lo_bits + k
 
     const int li = (int)(threadIdx.x & (LPB - 1));
     const int64_t ntiles = (nb + blocks_per_wg - 1) / blocks_per_wg;
@@ -107,11 +140,12 @@ __global__ __launch_bounds__(kThreads) void mx_fast_kernel(const uint16_t* __res
         const float s = mx_shared_scale<F16>(amax, p);
         const float rs = 1.0f / s;
 
-        float out[kV];
+        uint32_t y2[8];
         uint32_t cout[kV];
         if (__builtin_expect((m2 > 0x7c00u) | !(s > 0.f && s < __builtin_inff()), 0)) {
             // a NaN in the block, or a scale that rounds to 0 or inf in fp16 (an 8-bit
             // scale exponent): the generic element path
+            float out[kV];
 #pragma unroll
             for (int i = 0; i < kV; ++i) {
                 const float v = F16::load((uint16_t)(i & 1 ? w[i / 2] >> 16 : w[i / 2] & 0xffffu));
@@ -119,36 +153,62 @@ __global__ __launch_bounds__(kThreads) void mx_fast_kernel(const uint16_t* __res
                 const float q = elem_quant<F16, M>(yv, cout[i]);
                 out[i] = F16::round(q * s);
             }
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                y2[i] = (uint32_t)F16::store(out[2 * i]) | ((uint32_t)F16::store(out[2 * i + 1]) << 16);
         } else {
-            uint32_t key[kV];
-            float pmin = 65504.f;
+            // u = R16(|x| / s) of each element, packed in pairs like x: for a power-of-two
+            // scale the product is exact; for an FP scale R16(|x| * R32(1/s)) (one
+            // rounding) equals R16(|x| / s) unless the quotient is below 2^-14
+            uint32_t u2[8];
 #pragma unroll
-            for (int i = 0; i < kV; ++i) {
-                const float a = fabsf(F16::load((uint16_t)(i & 1 ? w[i / 2] >> 16 : w[i / 2] & 0xffffu)));
-                const float pr = a * rs;
-                pmin = fminf(pmin, pr);
-                key[i] = F16::store(pr);   // R16(|x| * 1/s)
+            for (int i = 0; i < 8; ++i) {
+                u2[i] = mix_lo(w[i], rs);
+                mix_hi(u2[i], w[i], rs);
             }
-            if (!p.pot && pmin < 6.103515625e-05f) {   // fp16 subnormal quotients can be exact ties: divide
+            if (!p.pot) {
+                u16x2_t mn = __builtin_bit_cast(u16x2_t, u2[0]);
 #pragma unroll
-                for (int i = 0; i < kV; ++i) {
-                    const float a = fabsf(F16::load((uint16_t)(i & 1 ? w[i / 2] >> 16 : w[i / 2] & 0xffffu)));
-                    if (a * rs < 6.103515625e-05f) key[i] = F16::store(a / s);
+                for (int i = 1; i < 8; ++i) mn = __builtin_elementwise_min(mn, __builtin_bit_cast(u16x2_t, u2[i]));
+                if ((mn.x <= 0x0400u) | (mn.y <= 0x0400u)) {   // near or in the subnormal range: divide
+#pragma unroll
+                    for (int i = 0; i < kV; ++i) {
+                        const uint32_t key = i & 1 ? u2[i / 2] >> 16 : u2[i / 2] & 0xffffu;
+                        if (key <= 0x0400u) {
+                            const float a = fabsf(F16::load((uint16_t)(i & 1 ? w[i / 2] >> 16 : w[i / 2] & 0xffffu)));
+                            const uint32_t k2 = F16::store(a / s);
+                            u2[i / 2] = i & 1 ? (u2[i / 2] & 0xffffu) | (k2 << 16) : (u2[i / 2] & 0xffff0000u) | k2;
+                        }
+                    }
                 }
             }
 #pragma unroll
-            for (int i = 0; i < kV; ++i) {
-                int k;   // clamp to [-1, n]; word k + 1
-                asm("v_med3_i32 %0, %1, -1, %2" : "=v"(k) : "v"((int)key[i] - (int)lo_bits), "s"(n));
-                const uint32_t e = lut[k + 1];
-                const uint32_t xs = (i & 1 ? w[i / 2] >> 31 : (w[i / 2] >> 15) & 1u) & (key[i] != 0u ? 1u : 0u);
-                const float o = F16::round(F16::load((uint16_t)(e >> 16)) * s);
-                out[i] = xs ? -o : o;
-                cout[i] = (e & 0xffu) | (xs << (M + 2));
+            for (int i = 0; i < 8; ++i) {
+                uint32_t lv[2];
+                u16x2_t q2;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int key = (int)(h ? u2[i] >> 16 : u2[i] & 0xffffu);
+                    int k;   // word index k + 1 clamped to [0, n + 1] in one v_med3_i32
+                    asm("v_med3_i32 %0, %1, 0, %2" : "=v"(k) : "v"(key - (int)lo_m1), "s"(n + 1));
+                    lv[h] = lvls[k];
+                    q2[h] = mags[lv[h]];
+                }
+                uint32_t o2 = mix_lo(__builtin_bit_cast(uint32_t, q2), s);   // R16(q * s): exact product
+                mix_hi(o2, __builtin_bit_cast(uint32_t, q2), s);
+                // the sign of x unless u is +-0 (the reference's u == 0 gives +0 and code 0):
+                // bit 15 of each half of u2 + 0x7fff7fff is set iff that half is nonzero
+                // (u <= 0x7c00, so no carry crosses the halves)
+                const uint32_t sg = w[i] & (u2[i] + 0x7fff7fffu) & 0x80008000u;
+                y2[i] = o2 | sg;
+                cout[2 * i] = lv[0] | (((sg >> 15) & 1u) << (M + 2));
+                cout[2 * i + 1] = lv[1] | ((sg >> 31) << (M + 2));
             }
         }
         if (valid) {
-            store16<F16>(y + off, out);
+            u32x4_t* yq = reinterpret_cast<u32x4_t*>(y + off);
+            __builtin_nontemporal_store((u32x4_t){y2[0], y2[1], y2[2], y2[3]}, yq);
+            __builtin_nontemporal_store((u32x4_t){y2[4], y2[5], y2[6], y2[7]}, yq + 1);
             if (codes) {
                 if constexpr (M == 1) {
                     uint32_t w0 = 0, w1 = 0;
@@ -185,18 +245,20 @@ int build_mx_slot(int slot, int n, uint32_t lo_bits, hipStream_t st) {
     hipError_t e = hipGetLastError();
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     if (e != hipSuccess) return -hbq_fail(HBQ_ERR_HIP, "MX level table build failed: %s", hipGetErrorString(e));
-    int status = -1;
+    int status = -1, bad = -1;
     e = hipMemcpyFromSymbol(&status, HIP_SYMBOL(g_mx_status), sizeof(int), sizeof(int) * slot,
                             hipMemcpyDeviceToHost);
+    if (e == hipSuccess)
+        e = hipMemcpyFromSymbol(&bad, HIP_SYMBOL(g_mx_bad), sizeof(int), sizeof(int) * slot, hipMemcpyDeviceToHost);
     if (e != hipSuccess)
         return -hbq_fail(HBQ_ERR_HIP, "MX level table status read failed: %s", hipGetErrorString(e));
-    return status;
+    return status > bad ? status : bad;
 }
 
 template <int M, int LPB>
 int launch_mx_fast(const void* x, void* y, void* scales, void* codes, int64_t nb, int slot, int n, uint32_t lo_bits,
                    const MxParams& p, int dev, hipStream_t st) {
-    const size_t lds = (size_t)(n + 2) * 4;
+    const size_t lds = (size_t)((kMxMagBytes + n + 2 + 15) / 16) * 16;
     auto kern = mx_fast_kernel<M, LPB>;
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kThreads, lds) != hipSuccess || per_cu <= 0)
@@ -207,7 +269,7 @@ int launch_mx_fast(const void* x, void* y, void* scales, void* codes, int64_t nb
     const int64_t rounds = (ntiles + resident - 1) / resident;
     const int64_t grid = (ntiles + rounds - 1) / rounds;
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), lds, st, (const uint16_t*)x, (uint16_t*)y,
-                       (uint16_t*)scales, (uint8_t*)codes, nb, slot, n, lo_bits, p);
+                       (uint16_t*)scales, (uint8_t*)codes, nb, slot, n, lo_bits - 1u, p);
     return 1;
 }
 

@@ -84,3 +84,18 @@ def test_elem_max_reciprocal(dt):
         approx = _round_T((a * (np.float32(1.0) / np.float32(em))).astype(np.float32), dt)
         lo, hi = np.float32(2.0 ** -14), np.float32(61440.0)
         assert np.array_equal(np.clip(exact, lo, hi), np.clip(approx, lo, hi)), em
+
+
+def test_fp16_single_rounding_reciprocal_product():
+    """R16 of the exact product x * R32(1/s) (one rounding, as v_fma_mix computes it) equals
+    R16(x / s) for every fp16 x and every E5M3 scale s, wherever the quotient is not in the
+    fp16 subnormal range (the NVFP element path of the table-driven MXFP kernel)."""
+    x = _values(torch.float16).astype(np.float64)
+    bad = 0
+    for s in [(1 + m / 8) * 2.0 ** e for e in range(-14, 16) for m in range(8)]:
+        r = np.float64(np.float32(1.0) / np.float32(s))
+        exact = _round_T((x / s).astype(np.float32), torch.float16)   # float64 quotient -> f32 -> f16: innocuous
+        once = (x * r).astype(np.float16).astype(np.float32)   # exact float64 product, one rounding to fp16
+        use = np.abs(x * r) >= 2.0 ** -14
+        bad += int((exact[use] != once[use]).sum())
+    assert bad == 0
