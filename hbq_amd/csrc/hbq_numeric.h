@@ -6,6 +6,7 @@
 // compiled with -ffp-contract=off: a fused multiply-add anywhere below would
 // change results.
 #pragma once
+#include <type_traits>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -72,13 +73,25 @@ __device__ __forceinline__ void round2(float a, float b, float& ra, float& rb) {
 // True exponent e of a positive finite float (2^e <= a < 2^(e+1)), subnormals included.
 __device__ __forceinline__ int binade(float a) { return __builtin_amdgcn_frexp_expf(a) - 1; }
 
+// Where log2_exponent reads its per-binade thresholds: the __constant__ tables
+// of log2_tables.h (ConstLog2), or copies of T's two tables that a kernel keeps
+// in LDS (LdsLog2: entry e - EMIN of T), which saves a dependent global load.
+struct ConstLog2 {};
+struct LdsLog2 {
+    const float* floor_thr;
+    const float* round_thr;
+};
+
 // floor(R_T(log2 a)) (round_mode 0) or rint(R_T(log2 a)) (round_mode 1) for a
 // positive finite T value a, from the per-binade thresholds in log2_tables.h.
-template <class T>
-__device__ __forceinline__ float log2_exponent(float a, int round_mode) {
+template <class T, class Tab = ConstLog2>
+__device__ __forceinline__ float log2_exponent(float a, int round_mode, Tab tab = Tab()) {
     int e = binade(a);
     float thr;
-    if (T::dt == kF16) {
+    if constexpr (std::is_same<Tab, LdsLog2>::value) {
+        const int i = e - (T::dt == kF16 ? HBQ_L2T_F16_EMIN : T::dt == kBF16 ? HBQ_L2T_BF16_EMIN : HBQ_L2T_F32_EMIN);
+        thr = round_mode ? tab.round_thr[i] : tab.floor_thr[i];
+    } else if (T::dt == kF16) {
         int i = e - HBQ_L2T_F16_EMIN;
         thr = round_mode ? kLog2RoundF16[i] : kLog2FloorF16[i];
     } else if (T::dt == kBF16) {
@@ -105,8 +118,8 @@ struct ScaleFmt {
     int e4m3;            // E4M3 saturates at +-448
 };
 
-template <class T>
-__device__ __forceinline__ float scale_quant(float s, const ScaleFmt& f) {
+template <class T, class Tab = ConstLog2>
+__device__ __forceinline__ float scale_quant(float s, const ScaleFmt& f, Tab tab = Tab()) {
     // clip (NaN passes through)
     s = s < f.lo ? f.lo : (s > f.hi ? f.hi : s);
     s = T::round(s);
@@ -116,7 +129,7 @@ __device__ __forceinline__ float scale_quant(float s, const ScaleFmt& f) {
     bool promote = (a < f.minn) && (a >= f.thr);
     bool sub = f.allow_sub && (a < f.thr) && !is_zero;
     bool under = !f.allow_sub && (a < f.thr) && !is_zero;
-    float fe = a == __builtin_inff() ? a : log2_exponent<T>(is_zero ? 1.f : a, 0);
+    float fe = a == __builtin_inff() ? a : log2_exponent<T>(is_zero ? 1.f : a, 0, tab);
     float e = fe < f.emin ? f.emin : (fe > f.emax ? f.emax : fe);
     // division by a power of two = multiplication by its exact reciprocal
     float rp2 = pow2f(-(int)e);

@@ -105,7 +105,11 @@ __global__ __launch_bounds__(kThreads) void mx_fast_kernel(const uint16_t* __res
         uint4* dst = reinterpret_cast<uint4*>(tab);
         for (int i = threadIdx.x; i < (kMxMagBytes + n + 2 + 15) / 16; i += kThreads) dst[i] = src[i];
     }
+    // the fp16 log2 thresholds of the shared scale, after the table
+    float* l2t = reinterpret_cast<float*>(tab + (kMxMagBytes + n + 2 + 15) / 16 * 16);
+    for (int i = threadIdx.x; i < 80; i += kThreads) l2t[i] = i < 40 ? kLog2FloorF16[i] : kLog2RoundF16[i - 40];
     __syncthreads();
+    const LdsLog2 lt{l2t, l2t + 40};
     const uint16_t* mags = reinterpret_cast<const uint16_t*>(tab);
     const uint8_t* lvls = tab + kMxMagBytes;   // lvls[k + 1] for u with fp16 bits lo_bits + k
 
@@ -137,7 +141,7 @@ __global__ __launch_bounds__(kThreads) void mx_fast_kernel(const uint16_t* __res
             m2 = m2 > o ? m2 : o;
         }
         const float amax = F16::load((uint16_t)m2);
-        const float s = mx_shared_scale<F16>(amax, p);
+        const float s = mx_shared_scale<F16>(amax, p, lt);
         const float rs = 1.0f / s;
 
         uint32_t y2[8];
@@ -258,7 +262,7 @@ int build_mx_slot(int slot, int n, uint32_t lo_bits, hipStream_t st) {
 template <int M, int LPB>
 int launch_mx_fast(const void* x, void* y, void* scales, void* codes, int64_t nb, int slot, int n, uint32_t lo_bits,
                    const MxParams& p, int dev, hipStream_t st) {
-    const size_t lds = (size_t)((kMxMagBytes + n + 2 + 15) / 16) * 16;
+    const size_t lds = (size_t)((kMxMagBytes + n + 2 + 15) / 16) * 16 + 80 * sizeof(float);
     auto kern = mx_fast_kernel<M, LPB>;
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kThreads, lds) != hipSuccess || per_cu <= 0)

@@ -189,20 +189,20 @@ struct MxParams {
     float tscale;         // per-tensor scale, already rounded to T
 };
 
-template <class T>
-__device__ __forceinline__ float mx_shared_scale(float amax, const MxParams& p) {
+template <class T, class Tab = ConstLog2>
+__device__ __forceinline__ float mx_shared_scale(float amax, const MxParams& p, Tab tab = Tab()) {
     if (p.pot) {
         float v = T::round(amax + (amax == 0.f ? p.min_normal : 0.f));
         float se;
         if (v != v) se = v;
         else if (v == __builtin_inff()) se = __builtin_inff();
-        else se = log2_exponent<T>(v, p.use_round);
+        else se = log2_exponent<T>(v, p.use_round, tab);
         se = T::round(se - p.ele_emax);
         se = se < p.sc_emin ? p.sc_emin : (se > p.sc_emax ? p.sc_emax : se);
         if (se != se) return se;
         return T::round(pow2f((int)se));
     }
-    return scale_quant<T>(T::round(amax / p.ele_maxnorm), p.sf);
+    return scale_quant<T>(T::round(amax / p.ele_maxnorm), p.sf, tab);
 }
 
 struct HbqParams {
