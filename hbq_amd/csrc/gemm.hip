@@ -149,10 +149,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const uint16_t* __res
                     }
                 }
         } else {
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) fold_block<MODE, GN>(acc[i][j], H[i][j]);
+            fold_all<MODE, GN>(acc, H);
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i)

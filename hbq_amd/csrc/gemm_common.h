@@ -16,6 +16,9 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 namespace hbq_gemm {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -106,7 +109,25 @@ __device__ __forceinline__ h2_t sub_pair(float t0, float t1, float M) {
     return h;
 }
 
+// R16(t0 - M0) and R16(t1 - M1) packed in one register (two v_fma_mix)
+__device__ __forceinline__ h2_t sub_pair2(float t0, float M0, float t1, float M1) {
+    h2_t h;
+    asm("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,0]" : "=v"(h) : "v"(t0), "v"(M0));
+    asm("v_fma_mixhi_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,0]" : "+v"(h) : "v"(t1), "v"(M1));
+    return h;
+}
+
 __device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
+
+// mxfp8 (E3M4, s = 2^(ilogb(mx) - 3)) of one partial P with the group's subnormal
+// magic constant msub: the E3M4 grid step is 2^(ilogb P - 4) for |P| >= s / 4 and
+// s / 64 below, so M = 1.5 * 2^23 * step = max(1.5 * 2^(ilogb P + 19), msub) (as
+// float bit patterns, which order like the positive floats) and (P + M) - M is P
+// rounded to the grid, ties to even as the reference's nearbyintf.
+__device__ __forceinline__ float e3m4_magic(float P, uint32_t msub) {
+    const uint32_t mn = (__builtin_bit_cast(uint32_t, P) & 0x7f800000u) + (19u << 23) + 0x400000u;
+    return __builtin_bit_cast(float, mn > msub ? mn : msub);
+}
 
 // Fold the 16 fp32 partials of one 32x32 block into the fp16 accumulators H
 // (8 packed pairs; pair p holds registers 2p and 2p + 1, adjacent columns).
@@ -189,17 +210,67 @@ __device__ __forceinline__ void fold_block(const f16v& acc, h2_t* H) {
                 for (int p = 0; p < 8; ++p) H[p] = H[p] + cvt2(q[2 * p], q[2 * p + 1]);
             }
         } else {
-            float q[16];
+            // mxfp8: the fast path needs the group max in [2^-100, 2^100) (or zero), where
+            // the magic constants stay normal floats; a max with a mantissa of at least
+            // 1 + 31/32 (mx / s >= 15.75) can round to 16 s, which the clamp to
+            // R16(15.5 s) turns into the reference's 15.5 s
+            bool special8 = false, top8 = false;
 #pragma unroll
             for (int g = 0; g < NG; ++g) {
-                const float s = psum_scale(mxg[g], 3);
-#pragma unroll
-                for (int r = g * RPG; r < (g + 1) * RPG; ++r) q[r] = e3m4_qdq(acc[r], s);
+                special8 |= (mxg[g] >= 0x1p100f) | ((mxg[g] < 0x1p-100f) & (mxg[g] != 0.f));
+                top8 |= (__builtin_bit_cast(uint32_t, mxg[g]) & 0x7fffffu) >= 0x7c0000u;
             }
+            if (__builtin_expect(!wave_any(special8), 1)) {
+                auto run = [&](auto clamp_tag) __attribute__((always_inline)) {
+                    constexpr bool CLAMP = decltype(clamp_tag)::value;
 #pragma unroll
-            for (int p = 0; p < 8; ++p) H[p] = H[p] + cvt2(q[2 * p], q[2 * p + 1]);
+                    for (int g = 0; g < NG; ++g) {
+                        const uint32_t mb = __builtin_bit_cast(uint32_t, mxg[g]);
+                        const uint32_t sb = (mb & 0x7f800000u) - (3u << 23);   // s (wraps for mx = 0, harmless)
+                        const uint32_t msub = sb + (17u << 23) + 0x400000u;    // 1.5 * 2^23 * s / 64
+#pragma unroll
+                        for (int r = g * RPG; r < (g + 1) * RPG; r += 2) {
+                            const float M0 = e3m4_magic(acc[r], msub), M1 = e3m4_magic(acc[r + 1], msub);
+                            const float t0 = acc[r] + M0, t1 = acc[r + 1] + M1;
+                            h2_t q = sub_pair2(t0, M0, t1, M1);
+                            if constexpr (CLAMP) {
+                                const _Float16 c =
+                                    (_Float16)(15.5f * (mb != 0u ? __builtin_bit_cast(float, sb) : 1.0f));
+                                const h2_t hi = (h2_t){c, c};
+                                q = __builtin_elementwise_maximum(__builtin_elementwise_minimum(q, hi), -hi);
+                            }
+                            H[r / 2] = H[r / 2] + q;
+                        }
+                    }
+                };
+                if (__builtin_expect(!wave_any(top8), 1)) run(std::false_type{});
+                else run(std::true_type{});
+            } else {
+                float q[16];
+#pragma unroll
+                for (int g = 0; g < NG; ++g) {
+                    const float s = psum_scale(mxg[g], 3);
+#pragma unroll
+                    for (int r = g * RPG; r < (g + 1) * RPG; ++r) q[r] = e3m4_qdq(acc[r], s);
+                }
+#pragma unroll
+                for (int p = 0; p < 8; ++p) H[p] = H[p] + cvt2(q[2 * p], q[2 * p + 1]);
+            }
         }
     }
+}
+
+// fold_block over an R x C array of blocks with compile-time indices: the
+// blocks' accumulators must stay in registers, and a loop the compiler declines
+// to unroll (the exact paths make the body large) would index them dynamically
+// and move them to scratch memory.
+template <int MODE, int GN, int R, int C, int... B>
+__device__ __forceinline__ void fold_all_impl(f16v (&acc)[R][C], h2_t (&H)[R][C][8], std::integer_sequence<int, B...>) {
+    (fold_block<MODE, GN>(acc[B / C][B % C], H[B / C][B % C]), ...);
+}
+template <int MODE, int GN, int R, int C>
+__device__ __forceinline__ void fold_all(f16v (&acc)[R][C], h2_t (&H)[R][C][8]) {
+    fold_all_impl<MODE, GN>(acc, H, std::make_integer_sequence<int, R * C>{});
 }
 
 }  // namespace hbq_gemm

@@ -120,10 +120,7 @@ __global__ __launch_bounds__(NT, 1) void kernel(const uint16_t* __restrict__ A, 
                     }
                 }
         } else if constexpr (MODE != kFp32) {
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) fold_block<MODE, GN>(acc[i][j], H[i][j]);
+            fold_all<MODE, GN>(acc, H);
         }
     };
 
