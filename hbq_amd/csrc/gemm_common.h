@@ -149,7 +149,7 @@ __device__ __forceinline__ float e3m4_magic(float P, uint32_t msub) {
 // nonzero max outside [2^-100, 2^110), the whole wave takes the exact formula.
 // The branches depend on wave-wide ballots, so they are scalar branches.
 template <int MODE, int GN>
-__device__ __forceinline__ void fold_block(const f16v& acc, h2_t* H) {
+__device__ __forceinline__ void fold_block_impl(const f16v& acc, h2_t* H) {
     if constexpr (MODE == kGrouped) {
 #pragma unroll
         for (int p = 0; p < 8; ++p) H[p] = H[p] + cvt2(acc[2 * p], acc[2 * p + 1]);
@@ -257,6 +257,18 @@ __device__ __forceinline__ void fold_block(const f16v& acc, h2_t* H) {
                 for (int p = 0; p < 8; ++p) H[p] = H[p] + cvt2(q[2 * p], q[2 * p + 1]);
             }
         }
+    }
+}
+
+template <int MODE, int GN>
+__device__ __forceinline__ void fold_block(const f16v& acc, h2_t* H) {
+    fold_block_impl<MODE, GN>(acc, H);
+    // H is final here: without this the compiler may defer the packed adds of a
+    // psum group past the next K slice, keeping the 8 quantized pairs of every
+    // block live across it (64 extra registers, spills)
+    if constexpr (MODE != kGrouped) {
+#pragma unroll
+        for (int p = 0; p < 8; ++p) asm volatile("" : "+v"(H[p]));
     }
 }
 
