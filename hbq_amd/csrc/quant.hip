@@ -266,6 +266,35 @@ int dispatch_hbq(int mbit, int S, int l2b, const Geometry& g, const void* x, voi
 
 static int g_hbq_force_generic = 0;
 
+// ---------------------------------------------------------------------------
+// non-finite check of a GEMM output (the test of src/module.py:51-66 without a
+// host synchronization): flag = 1 if any element has an all-ones exponent
+// ---------------------------------------------------------------------------
+// em: the exponent fields of the elements of a 32-bit word (two 16-bit elements or one fp32)
+__global__ __launch_bounds__(kThreads) void nonfinite_kernel(const uint8_t* __restrict__ x, int64_t nbytes, int esize,
+                                                             uint32_t em, int* __restrict__ flag) {
+    const uint32_t elo = esize == 4 ? em : (em & 0xffffu), ehi = esize == 4 ? 0u : (em & 0xffff0000u);
+    auto bad_word = [&](uint32_t w) __attribute__((always_inline)) {
+        return ((w & elo) == elo) | (esize != 4 && (w & ehi) == ehi);
+    };
+    bool bad = false;
+    const int64_t nchunks = nbytes / 16;
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x; c < nchunks; c += stride) {
+        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x) + c);
+        bad |= bad_word(v.x) | bad_word(v.y) | bad_word(v.z) | bad_word(v.w);
+    }
+    // the last nbytes % 16 bytes (whole elements), by the first workgroup
+    if (blockIdx.x == 0) {
+        for (int64_t b = nchunks * 16 + (int64_t)threadIdx.x * esize; b < nbytes; b += (int64_t)kThreads * esize) {
+            uint32_t w = 0;
+            for (int k = 0; k < esize; ++k) w |= (uint32_t)x[b + k] << (8 * k);
+            bad |= esize == 4 ? bad_word(w) : ((w & elo) == elo);
+        }
+    }
+    if (bad) *flag = 1;
+}
+
 extern "C" {
 
 // Test hook: 1 routes every HBQ and MXFP / NVFP call to the generic kernels (so both can be checked).
@@ -432,6 +461,22 @@ int hbq_elem_quant(const void* x, void* y, void* codes, int64_t n, int dtype, in
 #undef ELEM_M
 #undef ELEM_CASE
     return hbq_check_launch("hbq_elem_quant");
+}
+
+int hbq_flag_nonfinite(const void* x, int64_t n, int dtype, int* flag, void* stream) {
+    hbq_clear_error();
+    if (dtype != kF16 && dtype != kBF16 && dtype != kF32) return hbq_fail(HBQ_ERR_INVALID, "bad dtype code %d", dtype);
+    if (n < 0 || flag == nullptr || (n > 0 && x == nullptr)) return hbq_fail(HBQ_ERR_INVALID, "bad arguments");
+    if (n == 0) return 0;
+    const int esize = dtype == kF32 ? 4 : 2;
+    if ((uintptr_t)x % 16) return hbq_fail(HBQ_ERR_INVALID, "input must be 16-byte aligned");
+    const uint32_t em = dtype == kF32 ? 0x7f800000u : (dtype == kF16 ? 0x7c007c00u : 0x7f807f80u);
+    const int64_t nbytes = n * esize;
+    int64_t grid = (nbytes / 16 + kThreads * 4 - 1) / (kThreads * 4);
+    grid = grid < 1 ? 1 : (grid > 2048 ? 2048 : grid);
+    hipLaunchKernelGGL(nonfinite_kernel, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream,
+                       (const uint8_t*)x, nbytes, esize, em, flag);
+    return hbq_check_launch("hbq_flag_nonfinite");
 }
 
 }  // extern "C"

@@ -13,10 +13,39 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import _lib
 from .quantizer import _QBase
 
 # Active deferred-check scopes (see deferred_finite_checks).
 _DEFERRED = []
+
+
+class _FlagBuffer:
+    """Device int32 flags, one per checked output, set to 1 by hbq_flag_nonfinite when
+    the output holds a NaN or inf (one fused pass over the output, no host sync)."""
+
+    CHUNK = 512
+
+    def __init__(self):
+        self.chunks = []
+        self.mods = []
+
+    def check(self, mod, y):
+        i = len(self.mods)
+        if i % self.CHUNK == 0:
+            self.chunks.append(torch.zeros(self.CHUNK, dtype=torch.int32, device=y.device))
+        flag = self.chunks[-1][i % self.CHUNK:]
+        yc = y if y.is_contiguous() and y.data_ptr() % 16 == 0 else y.contiguous()
+        _lib.check(_lib.lib().hbq_flag_nonfinite(_lib.ptr(yc), yc.numel(), _lib.DTYPE_CODE[yc.dtype],
+                                                 _lib.ptr(flag), _lib.stream_of(yc)))
+        self.mods.append(mod)
+
+    def bad(self):
+        """The modules whose output was not finite, in call order."""
+        if not self.mods:
+            return []
+        flags = torch.cat(self.chunks).cpu().tolist()
+        return [m for m, f in zip(self.mods, flags) if f]
 
 
 @contextlib.contextmanager
@@ -25,24 +54,23 @@ def deferred_finite_checks():
     instead of synchronizing per layer, and the scope raises on exit if any output was
     not finite.  The reference raises per layer (src/module.py:51-66); the error still
     reaches the caller before the forward returns, without a host sync per layer."""
-    flags = []
+    flags = _FlagBuffer()
     _DEFERRED.append(flags)
     try:
         yield
     finally:
         _DEFERRED.pop()
-    if flags:
-        ok = torch.stack([f for _, f in flags]).cpu()
-        for (mod, _), good in zip(flags, ok.tolist()):
-            if not good:
-                raise RuntimeError(
-                    f"Non-finite output from {type(mod).__name__}({mod.in_features} -> {mod.out_features}) "
-                    f"(found after the forward).\n"
-                    f"  activation quantizer: {type(mod.aq).__name__}\n"
-                    f"  weight quantizer:     {type(mod.wq).__name__}\n"
-                    f"  matmul:               {type(mod.ops).__name__ if mod.ops is not None else 'F.linear'}\n"
-                    "The quantization format cannot represent this layer's dynamic range: check the element and "
-                    "scale exponent bits and the block size of the quantization config.")
+    bad = flags.bad()
+    if bad:
+        mod = bad[0]
+        raise RuntimeError(
+            f"Non-finite output from {type(mod).__name__}({mod.in_features} -> {mod.out_features}) "
+            f"(found after the forward).\n"
+            f"  activation quantizer: {type(mod.aq).__name__}\n"
+            f"  weight quantizer:     {type(mod.wq).__name__}\n"
+            f"  matmul:               {type(mod.ops).__name__ if mod.ops is not None else 'F.linear'}\n"
+            "The quantization format cannot represent this layer's dynamic range: check the element and "
+            "scale exponent bits and the block size of the quantization config.")
 
 
 def same_quantizer(a, b):
@@ -80,8 +108,8 @@ class _QBaseLinear(nn.Linear):
 
     def _check_finite(self, y):
         # src/module.py:51-66: a non-finite GEMM output is an error of the format choice
-        if _DEFERRED:
-            _DEFERRED[-1].append((self, torch.isfinite(y).all()))
+        if _DEFERRED and y.is_cuda and y.dtype in _lib.DTYPE_CODE:
+            _DEFERRED[-1].check(self, y)
             return
         if bool(torch.isfinite(y).all()):
             return

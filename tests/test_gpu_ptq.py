@@ -85,3 +85,29 @@ def test_linear_nonfinite_raises(gpu):
         lin.weight.fill_(60000.0)
     with pytest.raises(RuntimeError, match="Non-finite output"):
         lin(torch.full((4, 128), 100.0, dtype=torch.float16, device=gpu))
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
+def test_flag_nonfinite(gpu, dt):
+    """hbq_flag_nonfinite: set for a NaN / +inf / -inf anywhere (the 16-byte body or the
+    tail), left alone for finite extremes (max normal, subnormals, -0)."""
+    from hbq_amd import _lib
+    L = _lib.lib()
+    big = torch.finfo(dt).max
+    for n in (1, 7, 8, 9, 1000, 3 * 4096 + 5):
+        base = torch.randn(n, device=gpu).to(dt)
+        base[0] = big
+        base[-1] = -big
+        if n > 2:
+            base[1] = torch.finfo(dt).tiny / 4   # subnormal
+            base[2] = -0.0
+        flag = torch.zeros(1, dtype=torch.int32, device=gpu)
+        _lib.check(L.hbq_flag_nonfinite(_lib.ptr(base), n, _lib.DTYPE_CODE[dt], _lib.ptr(flag), _lib.stream_of(base)))
+        assert int(flag.item()) == 0, n
+        for pos in sorted({0, n // 2, n - 1}):
+            for bad in (float("nan"), float("inf"), -float("inf")):
+                x = base.clone()
+                x[pos] = bad
+                flag.zero_()
+                _lib.check(L.hbq_flag_nonfinite(_lib.ptr(x), n, _lib.DTYPE_CODE[dt], _lib.ptr(flag), _lib.stream_of(x)))
+                assert int(flag.item()) == 1, (n, pos, bad)
