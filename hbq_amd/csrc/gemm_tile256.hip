@@ -30,8 +30,8 @@
 namespace hbq_gemm {
 namespace t256 {
 
-constexpr int TM = 256, TN = 256, TK = 64, NT = 512;
-constexpr int SLICE = TM * TK;   // halfs of one operand slice (32 KB)
+constexpr int TM = 256, TK = 64, NT = 512;
+constexpr int SLICE = TM * TK;   // halfs of one A slice (32 KB)
 
 // chunk c of row r sits at chunk position c ^ (r % 8) ^ ((r / 8) % 2): any 8
 // consecutive rows use 8 different positions, and any 16 consecutive rows 16
@@ -42,15 +42,22 @@ __device__ __forceinline__ int swz(int row, int chunk) { return row * TK + 8 * s
 
 // SMALLG: group_k < 64 (grouped accumulation with group_k 16 or 32, or group
 // partials), GS = group_k / 16 steps per group; otherwise SPG = group_k / 64
-// slices per group (K is a multiple of group_k)
-template <int MODE, int GN, bool SMALLG, int GS, int SPG>
+// slices per group (K is a multiple of group_k).  TN: tile width, 256 (waves
+// of 128 x 64) or 128 (waves of 64 x 64, for grids that 256-wide tiles would
+// leave short of the compute units).
+template <int MODE, int GN, bool SMALLG, int GS, int SPG, int TN>
 __global__ __launch_bounds__(NT, 1) void kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ W,
                                                 uint16_t* __restrict__ C, float* __restrict__ P, int M, int N, int K,
                                                 int gk, int tiles_m, int tiles_n) {
-    __shared__ __attribute__((aligned(1024))) uint16_t sA0[SLICE];
-    __shared__ __attribute__((aligned(1024))) uint16_t sW0[SLICE];
-    __shared__ __attribute__((aligned(1024))) uint16_t sA1[SLICE];
-    __shared__ __attribute__((aligned(1024))) uint16_t sW1[SLICE];
+    constexpr int WSL = TN * TK;          // halfs of one W slice
+    constexpr int NWN = TN / 64;          // waves across the tile's columns
+    constexpr int WROWS = TM * NWN / 8;   // rows of one wave (128 or 64)
+    constexpr int RB = WROWS / 32;        // 32-row blocks of one wave
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * SLICE + 2 * WSL];
+    uint16_t* const sA0 = smem;
+    uint16_t* const sA1 = smem + SLICE;
+    uint16_t* const sW0 = smem + 2 * SLICE;
+    uint16_t* const sW1 = smem + 2 * SLICE + WSL;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -67,8 +74,8 @@ __global__ __launch_bounds__(NT, 1) void kernel(const uint16_t* __restrict__ A, 
     const int tm = first + within % rows_in_band;
     const int tn = within / rows_in_band;
     const int m0 = tm * TM, n0 = tn * TN;
-    const int wm = (wave >> 2) * 128;   // wave's rows in the tile
-    const int wn = (wave & 3) * 64;     // wave's columns in the tile
+    const int wm = (wave / NWN) * WROWS;   // wave's rows in the tile
+    const int wn = (wave % NWN) * 64;      // wave's columns in the tile
 
     // ---- global -> LDS loads: wave w fills the 8-row groups w, w+8, w+16, w+24 of both slices ----
     // Buffer loads: the resource starts at the tile's first row and this
@@ -89,16 +96,17 @@ __global__ __launch_bounds__(NT, 1) void kernel(const uint16_t* __restrict__ A, 
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, la + (wave + 8 * i) * 8 * TK, 16, (int)voff[i], 0, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, lw + (wave + 8 * i) * 8 * TK, 16, (int)voff[i], 0, 0, 0);
+            if (i < TN / 64)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, lw + (wave + 8 * i) * 8 * TK, 16, (int)voff[i], 0, 0, 0);
         }
     };
 
-    f16v acc[2][4];     // [column block][row block]; fp32 partials of the current K group
-    h2_t H[2][4][8];    // fp16 accumulators
+    f16v acc[2][RB];     // [column block][row block]; fp32 partials of the current K group
+    h2_t H[2][RB][8];    // fp16 accumulators
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < RB; ++j)
 #pragma unroll
             for (int p = 0; p < 8; ++p) H[i][j][p] = (h2_t){(_Float16)0.f, (_Float16)0.f};
 
@@ -111,7 +119,7 @@ __global__ __launch_bounds__(NT, 1) void kernel(const uint16_t* __restrict__ A, 
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
+                for (int j = 0; j < RB; ++j) {
                     const int m = m0 + wm + 32 * j + (lane & 31);
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
@@ -145,16 +153,16 @@ __global__ __launch_bounds__(NT, 1) void kernel(const uint16_t* __restrict__ A, 
 #pragma unroll
         for (int s = 0; s < TK / 16; ++s) {
             const int cs = swz_pos(lane & 15, 2 * s + (lane >> 5)) << 4;   // swizzled chunk, bytes
-            h8 bop[2], aop[4];
+            h8 bop[2], aop[RB];
 #pragma unroll
             for (int i = 0; i < 2; ++i) bop[i] = *reinterpret_cast<const h8*>(lwb + i * 32 * (TK * 2) + cs);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) aop[j] = *reinterpret_cast<const h8*>(lab + j * 32 * (TK * 2) + cs);
+            for (int j = 0; j < RB; ++j) aop[j] = *reinterpret_cast<const h8*>(lab + j * 32 * (TK * 2) + cs);
             const bool zero = SMALLG ? (s % GS == 0) : (FRESH && s == 0);
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < RB; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bop[i], aop[j], zero ? (f16v){} : acc[i][j],
                                                                        0, 0, 0);
             if constexpr (SMALLG) {
@@ -205,13 +213,14 @@ __global__ __launch_bounds__(NT, 1) void kernel(const uint16_t* __restrict__ A, 
 
     if constexpr (MODE == kPartial) return;
 
-    // ---- store: each wave stages its 128x64 fp16 sub-tile (16 KB) in LDS, then writes full row segments ----
+    // ---- store: each wave stages its WROWS x 64 fp16 sub-tile in LDS, then writes full row segments ----
+    static_assert(8 * WROWS * 64 <= 2 * SLICE + 2 * WSL, "staging area");
     __syncthreads();
-    uint16_t* st = (wave < 2 ? sA0 : wave < 4 ? sW0 : wave < 6 ? sA1 : sW1) + (wave & 1) * (128 * 64);
+    uint16_t* st = smem + wave * (WROWS * 64);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < RB; ++j)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 h2_t lo, hi;
@@ -228,7 +237,7 @@ __global__ __launch_bounds__(NT, 1) void kernel(const uint16_t* __restrict__ A, 
             }
     __syncthreads();
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
+    for (int t = 0; t < WROWS / 8; ++t) {
         const int id = lane + 64 * t;
         const int row = id >> 3, ch = id & 7;
         const u32x4 v = *reinterpret_cast<const u32x4*>(st + swz(row, ch));
@@ -237,12 +246,12 @@ __global__ __launch_bounds__(NT, 1) void kernel(const uint16_t* __restrict__ A, 
     }
 }
 
-template <int MODE, int GN>
+template <int MODE, int GN, int TN>
 void launch(const void* A, const void* W, void* C, float* P, int M, int N, int K, int gk, hipStream_t st) {
     const int tm = (M + TM - 1) / TM, tn = (N + TN - 1) / TN;
     const dim3 grid(tm * tn), block(NT);
 #define T256_LAUNCH(SM, GS_, SPG_)                                                                              \
-    hipLaunchKernelGGL((kernel<MODE, GN, SM, GS_, SPG_>), grid, block, 0, st, (const uint16_t*)A,              \
+    hipLaunchKernelGGL((kernel<MODE, GN, SM, GS_, SPG_, TN>), grid, block, 0, st, (const uint16_t*)A,          \
                        (const uint16_t*)W, (uint16_t*)C, P, M, N, K, gk, tm, tn)
     if constexpr (MODE == kFp32) {
         T256_LAUNCH(false, 4, 1);
@@ -255,6 +264,34 @@ void launch(const void* A, const void* W, void* C, float* P, int M, int N, int K
 }
 
 }  // namespace t256
+
+template <int TN>
+static int launch_w(int mode, int gn, const void* A, const void* B, void* C, float* P, int M, int N, int K, int gk,
+                    hipStream_t st) {
+    using namespace t256;
+    switch (mode) {
+        case kGrouped: launch<kGrouped, 4, TN>(A, B, C, P, M, N, K, gk, st); return 1;
+        case kFp32: launch<kFp32, 4, TN>(A, B, C, P, M, N, K, gk, st); return 1;
+        case kPartial: launch<kPartial, 4, TN>(A, B, C, P, M, N, K, gk, st); return 1;
+        case kInt8:
+            switch (gn) {
+                case 4: launch<kInt8, 4, TN>(A, B, C, P, M, N, K, gk, st); return 1;
+                case 8: launch<kInt8, 8, TN>(A, B, C, P, M, N, K, gk, st); return 1;
+                case 16: launch<kInt8, 16, TN>(A, B, C, P, M, N, K, gk, st); return 1;
+                case 32: launch<kInt8, 32, TN>(A, B, C, P, M, N, K, gk, st); return 1;
+            }
+            return 0;
+        case kFp8:
+            switch (gn) {
+                case 4: launch<kFp8, 4, TN>(A, B, C, P, M, N, K, gk, st); return 1;
+                case 8: launch<kFp8, 8, TN>(A, B, C, P, M, N, K, gk, st); return 1;
+                case 16: launch<kFp8, 16, TN>(A, B, C, P, M, N, K, gk, st); return 1;
+                case 32: launch<kFp8, 32, TN>(A, B, C, P, M, N, K, gk, st); return 1;
+            }
+            return 0;
+    }
+    return 0;
+}
 
 int launch_tile256(int mode, int gn, const void* A, const void* B, void* C, float* P, int M, int N, int K, int gk,
                    int b_is_nk, hipStream_t st) {
@@ -275,28 +312,10 @@ int launch_tile256(int mode, int gn, const void* A, const void* B, void* C, floa
             hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
             cus = n;
     }
-    if ((int64_t)((M + TM - 1) / TM) * ((N + TN - 1) / TN) < cus) return 0;
-    switch (mode) {
-        case kGrouped: launch<kGrouped, 4>(A, B, C, P, M, N, K, gk, st); return 1;
-        case kFp32: launch<kFp32, 4>(A, B, C, P, M, N, K, gk, st); return 1;
-        case kPartial: launch<kPartial, 4>(A, B, C, P, M, N, K, gk, st); return 1;
-        case kInt8:
-            switch (gn) {
-                case 4: launch<kInt8, 4>(A, B, C, P, M, N, K, gk, st); return 1;
-                case 8: launch<kInt8, 8>(A, B, C, P, M, N, K, gk, st); return 1;
-                case 16: launch<kInt8, 16>(A, B, C, P, M, N, K, gk, st); return 1;
-                case 32: launch<kInt8, 32>(A, B, C, P, M, N, K, gk, st); return 1;
-            }
-            return 0;
-        case kFp8:
-            switch (gn) {
-                case 4: launch<kFp8, 4>(A, B, C, P, M, N, K, gk, st); return 1;
-                case 8: launch<kFp8, 8>(A, B, C, P, M, N, K, gk, st); return 1;
-                case 16: launch<kFp8, 16>(A, B, C, P, M, N, K, gk, st); return 1;
-                case 32: launch<kFp8, 32>(A, B, C, P, M, N, K, gk, st); return 1;
-            }
-            return 0;
-    }
+    const int64_t tm = (M + TM - 1) / TM;
+    if (tm * ((N + 255) / 256) >= cus) return launch_w<256>(mode, gn, A, B, C, P, M, N, K, gk, st);
+    // 256-wide tiles would leave compute units idle: 128-wide tiles if they fill the chip
+    if (tm * ((N + 127) / 128) >= cus) return launch_w<128>(mode, gn, A, B, C, P, M, N, K, gk, st);
     return 0;
 }
 

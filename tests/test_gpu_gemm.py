@@ -234,13 +234,15 @@ def test_transpose16(gpu, shape):
 @pytest.mark.parametrize("op,gk,gn", [("fp32", 0, 0), ("grouped", 128, 0), ("mxint8", 128, 32), ("mxint8", 256, 16),
                                       ("mxint8", 128, 4), ("mxfp8", 128, 32), ("mxfp8", 256, 8)])
 @pytest.mark.parametrize("K", [256, 512])
-def test_large_tile_kernel_bit_identical(gpu, op, gk, gn, K):
-    """At shapes with enough 256x256 tiles to fill the chip (16 x 16 here, the last tile row
-    ragged) W[N,K] runs on the 256x256 kernel, while B[K,N] without the transpose runs on the
-    128x128 kernel that the oracle tests pin: the same bits."""
+@pytest.mark.parametrize("M", [4000, 2000])
+def test_large_tile_kernel_bit_identical(gpu, op, gk, gn, K, M):
+    """At shapes with enough 256-row tiles to fill the chip W[N,K] runs on the 256-row kernel:
+    256 x 256 tiles at M = 4000 (16 x 16 tiles), 256 x 128 tiles at M = 2000 (8 x 32; 256-wide
+    tiles would give only 128), the last tile row ragged in both.  B[K,N] without the transpose
+    runs on the 128x128 kernel that the oracle tests pin: the same bits."""
     from hbq_amd import blockquant_ext as ext
-    M, N = 4000, 4096
-    print(f"large tiles {op} gk={gk} gn={gn} K={K}", flush=True)
+    N = 4096
+    print(f"large tiles {op} gk={gk} gn={gn} K={K} M={M}", flush=True)
     A = synth(M, K, 51, "f16").to(gpu)
     B = synth(K, N, 52, "f16", std=0.02).to(gpu)
     W = B.t().contiguous()
