@@ -235,7 +235,7 @@ def prefill_extra(dev, T=2048, iters=3):
     """one prefill of T tokens through Llama-3-8B (32 layers, random N(0, 0.02)
     weights, fp16) with the HBQ-A + KV quantization points; weights quantized once beforehand."""
     from hbq_amd.llama import LlamaConfig, LlamaForCausalLM
-    from hbq_amd.ops import use_hip_fp32_gemm
+    from hbq_amd.ops import stack_qkv_gemms, use_hip_fp32_gemm
     from hbq_amd.ptq import PTQ
     cfg = LlamaConfig()
     with torch.device(dev):
@@ -244,6 +244,7 @@ def prefill_extra(dev, T=2048, iters=3):
     p = PTQ(HBQ_A_KV, m)
     p.inject_quantizers()
     use_hip_fp32_gemm(m)          # the seven linears of every layer on the HIP GEMM (fp32 accumulation)
+    stack_qkv_gemms(m)            # q, k, v as one GEMM (N = 4096 + 1024 + 1024; the same bits)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     p.static_quant_wgt()

@@ -31,7 +31,7 @@ SIGNATURES = {
     "hbq_gemm_blockquant_mxfp8": ([_P, _P, _P, _I64, _I64, _I64, _I, _I, _I, _P], _I),
     "hbq_gemm_group_partials": ([_P, _P, _P, _I64, _I64, _I64, _I, _I, _P], _I),
     "hbq_transpose16": ([_P, _P, _I64, _I64, _P], _I),
-    "hbq_flag_nonfinite": ([_P, _I64, _I, _P, _P], _I),
+    "hbq_flag_nonfinite": ([_P, _I64, _I64, _I64, _I, _P, _P], _I),
 }
 
 

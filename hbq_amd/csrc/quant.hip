@@ -268,28 +268,33 @@ static int g_hbq_force_generic = 0;
 
 // ---------------------------------------------------------------------------
 // non-finite check of a GEMM output (the test of src/module.py:51-66 without a
-// host synchronization): flag = 1 if any element has an all-ones exponent
+// host synchronization): flag = 1 if any element has an all-ones exponent.
+// rows x cols elements, row stride ld; VEC: every row start 16-byte aligned and
+// cols * esize a multiple of 16 (16-byte loads), else one element per load.
 // ---------------------------------------------------------------------------
-// em: the exponent fields of the elements of a 32-bit word (two 16-bit elements or one fp32)
-__global__ __launch_bounds__(kThreads) void nonfinite_kernel(const uint8_t* __restrict__ x, int64_t nbytes, int esize,
-                                                             uint32_t em, int* __restrict__ flag) {
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void nonfinite_kernel(const uint8_t* __restrict__ x, int64_t rows, int64_t cols,
+                                                             int64_t ld, int esize, uint32_t em,
+                                                             int* __restrict__ flag) {
+    // em: the exponent fields of the elements of a 32-bit word (two 16-bit elements or one fp32)
     const uint32_t elo = esize == 4 ? em : (em & 0xffffu), ehi = esize == 4 ? 0u : (em & 0xffff0000u);
     auto bad_word = [&](uint32_t w) __attribute__((always_inline)) {
         return ((w & elo) == elo) | (esize != 4 && (w & ehi) == ehi);
     };
     bool bad = false;
-    const int64_t nchunks = nbytes / 16;
-    const int64_t stride = (int64_t)gridDim.x * kThreads;
-    for (int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x; c < nchunks; c += stride) {
-        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x) + c);
-        bad |= bad_word(v.x) | bad_word(v.y) | bad_word(v.z) | bad_word(v.w);
-    }
-    // the last nbytes % 16 bytes (whole elements), by the first workgroup
-    if (blockIdx.x == 0) {
-        for (int64_t b = nchunks * 16 + (int64_t)threadIdx.x * esize; b < nbytes; b += (int64_t)kThreads * esize) {
-            uint32_t w = 0;
-            for (int k = 0; k < esize; ++k) w |= (uint32_t)x[b + k] << (8 * k);
-            bad |= esize == 4 ? bad_word(w) : ((w & elo) == elo);
+    const int64_t per_row = VEC ? cols * esize / 16 : cols;   // units per row
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        const uint8_t* row = x + r * ld * esize;
+        for (int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x; c < per_row; c += (int64_t)gridDim.x * kThreads) {
+            if constexpr (VEC) {
+                const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row) + c);
+                bad |= bad_word(v.x) | bad_word(v.y) | bad_word(v.z) | bad_word(v.w);
+            } else {
+                uint32_t w;
+                if (esize == 4) w = *reinterpret_cast<const uint32_t*>(row + c * 4);
+                else w = *reinterpret_cast<const uint16_t*>(row + c * 2);
+                bad |= (w & elo) == elo;
+            }
         }
     }
     if (bad) *flag = 1;
@@ -463,19 +468,33 @@ int hbq_elem_quant(const void* x, void* y, void* codes, int64_t n, int dtype, in
     return hbq_check_launch("hbq_elem_quant");
 }
 
-int hbq_flag_nonfinite(const void* x, int64_t n, int dtype, int* flag, void* stream) {
+int hbq_flag_nonfinite(const void* x, int64_t rows, int64_t cols, int64_t ld, int dtype, int* flag, void* stream) {
     hbq_clear_error();
     if (dtype != kF16 && dtype != kBF16 && dtype != kF32) return hbq_fail(HBQ_ERR_INVALID, "bad dtype code %d", dtype);
-    if (n < 0 || flag == nullptr || (n > 0 && x == nullptr)) return hbq_fail(HBQ_ERR_INVALID, "bad arguments");
-    if (n == 0) return 0;
+    if (rows < 0 || cols < 0 || ld < cols || flag == nullptr) return hbq_fail(HBQ_ERR_INVALID, "bad arguments");
+    if (rows == 0 || cols == 0) return 0;
+    if (x == nullptr) return hbq_fail(HBQ_ERR_INVALID, "null tensor pointer");
     const int esize = dtype == kF32 ? 4 : 2;
-    if ((uintptr_t)x % 16) return hbq_fail(HBQ_ERR_INVALID, "input must be 16-byte aligned");
     const uint32_t em = dtype == kF32 ? 0x7f800000u : (dtype == kF16 ? 0x7c007c00u : 0x7f807f80u);
-    const int64_t nbytes = n * esize;
-    int64_t grid = (nbytes / 16 + kThreads * 4 - 1) / (kThreads * 4);
-    grid = grid < 1 ? 1 : (grid > 2048 ? 2048 : grid);
-    hipLaunchKernelGGL(nonfinite_kernel, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream,
-                       (const uint8_t*)x, nbytes, esize, em, flag);
+    if (ld == cols) {   // contiguous: one long row
+        cols *= rows;
+        ld = cols;
+        rows = 1;
+    }
+    const bool vec = (uintptr_t)x % 16 == 0 && (ld * esize) % 16 == 0 && (cols * esize) % 16 == 0;
+    const int64_t per_row = vec ? cols * esize / 16 : cols;
+    // about 4 units per thread, at most 2048 workgroups
+    int64_t gx = (per_row + kThreads * 4 - 1) / (kThreads * 4);
+    gx = gx > 2048 ? 2048 : gx;
+    int64_t gy = 2048 / gx;
+    gy = gy > rows ? rows : (gy > 65535 ? 65535 : gy);
+    const dim3 grid((unsigned)gx, (unsigned)gy);
+    if (vec)
+        hipLaunchKernelGGL(nonfinite_kernel<true>, grid, dim3(kThreads), 0, (hipStream_t)stream,
+                           (const uint8_t*)x, rows, cols, ld, esize, em, flag);
+    else
+        hipLaunchKernelGGL(nonfinite_kernel<false>, grid, dim3(kThreads), 0, (hipStream_t)stream,
+                           (const uint8_t*)x, rows, cols, ld, esize, em, flag);
     return hbq_check_launch("hbq_flag_nonfinite");
 }
 

@@ -17,7 +17,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn as nn
 
-from .module import _QBaseLinear, deferred_finite_checks, same_quantizer
+from .module import _QBaseLinear, deferred_finite_checks, forward_quantized_stacked, same_quantizer
 
 
 @dataclass
@@ -89,6 +89,8 @@ class QLlamaAttention(nn.Module):
         self.quant_v_cache = False
         self.kv_quantizer = None
         self.attn_wgt_quantizer = None
+        # one GEMM over the stacked q/k/v weights when their operators allow it (same bits)
+        self.stack_qkv = False
 
     def manual_sdpa(self, q, k, v):
         """Causal softmax(q k^T / sqrt(d)) v with the attention weights quantized after the
@@ -109,7 +111,10 @@ class QLlamaAttention(nn.Module):
         if same_quantizer(qp.aq, kp.aq) and same_quantizer(qp.aq, vp.aq):
             # q, k and v quantize the same input with the same function: quantize it once
             xq = qp.aq(x)
-            q, k, v = qp.forward_quantized(xq), kp.forward_quantized(xq), vp.forward_quantized(xq)
+            if self.stack_qkv:
+                q, k, v = forward_quantized_stacked((qp, kp, vp), xq)
+            else:
+                q, k, v = qp.forward_quantized(xq), kp.forward_quantized(xq), vp.forward_quantized(xq)
         else:
             q, k, v = qp(x), kp(x), vp(x)
         q = q.view(b, T, self.num_heads, self.head_dim).transpose(1, 2)

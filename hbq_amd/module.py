@@ -35,9 +35,11 @@ class _FlagBuffer:
         if i % self.CHUNK == 0:
             self.chunks.append(torch.zeros(self.CHUNK, dtype=torch.int32, device=y.device))
         flag = self.chunks[-1][i % self.CHUNK:]
-        yc = y if y.is_contiguous() and y.data_ptr() % 16 == 0 else y.contiguous()
-        _lib.check(_lib.lib().hbq_flag_nonfinite(_lib.ptr(yc), yc.numel(), _lib.DTYPE_CODE[yc.dtype],
-                                                 _lib.ptr(flag), _lib.stream_of(yc)))
+        y2 = y.reshape(-1, y.shape[-1]) if y.dim() != 2 else y   # a column slice of a wider output stays a view
+        if y2.stride(-1) != 1:
+            y2 = y2.contiguous()
+        _lib.check(_lib.lib().hbq_flag_nonfinite(_lib.ptr(y2), y2.shape[0], y2.shape[1], y2.stride(0),
+                                                 _lib.DTYPE_CODE[y2.dtype], _lib.ptr(flag), _lib.stream_of(y2)))
         self.mods.append(mod)
 
     def bad(self):
@@ -81,6 +83,73 @@ def same_quantizer(a, b):
     keys = ("ebit", "mbit", "sc_ebit", "sc_mbit", "block_size", "per_tensor_scale", "scale_allow_subnormal",
             "use_round", "use_ceil", "l2_block_size", "l2_sc_bit", "l2_scheme")
     return all(getattr(a, k, None) == getattr(b, k, None) for k in keys)
+
+
+def _fusable(mods):
+    """True when linears fed one quantized input can run as one GEMM over their stacked weights
+    and give each output column the same bits as their own GEMMs: a HIP operator of one type and
+    settings on all of them (each output column of those kernels depends only on its own weight
+    row), fp16 weights with one K on one GPU, no bias, and partial-sum blocks (quant_block_size
+    columns) that never straddle two linears."""
+    from .ops import FP16AccumMatMul, FP32AccumMatMul
+    o = mods[0].ops
+    if type(o) not in (FP16AccumMatMul, FP32AccumMatMul):
+        return False
+    w0 = mods[0].weight
+    for m in mods:
+        if type(m.ops) is not type(o) or any(getattr(m.ops, k, None) != getattr(o, k, None)
+                                             for k in ("group_size", "quant_block_size")):
+            return False
+        w = m.weight
+        if m.bias is not None or w.dtype != torch.float16 or not w.is_cuda or w.device != w0.device \
+                or w.dim() != 2 or w.shape[1] != w0.shape[1] or not w.is_contiguous():
+            return False
+    qb = getattr(o, "quant_block_size", None)
+    return qb is None or all(m.out_features % qb == 0 for m in mods[:-1])
+
+
+def _stacked_weight(mods):
+    """The weights of `mods` as consecutive row ranges of one [sum N, K] tensor.  Built on first
+    use by moving each weight into the stack (its parameter then views its rows: no memory is
+    added, and in-place updates of a weight land in the stack); built again when a weight has
+    been replaced (assignment to .data, .to(), a new Parameter)."""
+    W = mods[0].__dict__.get("_hbq_stack")
+    if W is not None:
+        off = 0
+        for m in mods:
+            w = m.weight
+            if w.data_ptr() != W.data_ptr() + off * W.stride(0) * W.element_size() or w.shape[0] != m.out_features \
+                    or w.shape[1] != W.shape[1] or w.device != W.device:
+                break
+            off += w.shape[0]
+        else:
+            if off == W.shape[0]:
+                return W
+    with torch.no_grad():
+        W = torch.cat([m.weight.detach() for m in mods])
+        off = 0
+        for m in mods:
+            n = m.weight.shape[0]
+            m.weight.data = W[off:off + n]
+            off += n
+    mods[0].__dict__["_hbq_stack"] = W
+    return W
+
+
+def forward_quantized_stacked(mods, xq):
+    """[m.forward_quantized(xq) for m in mods] as one GEMM over the stacked weights when the
+    linears allow it (same bits per output column), else one GEMM each.  The outputs are
+    column slices of the one result; each gets its module's finiteness check and yq."""
+    if len(mods) < 2 or not _fusable(mods):
+        return [m.forward_quantized(xq) for m in mods]
+    y = mods[0].ops(xq, _stacked_weight(mods), None)
+    outs, off = [], 0
+    for m in mods:
+        ym = y[..., off:off + m.out_features]
+        off += m.out_features
+        m._check_finite(ym)
+        outs.append(m.yq(ym))
+    return outs
 
 
 class _QBaseLinear(nn.Linear):

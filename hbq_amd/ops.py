@@ -76,3 +76,16 @@ def use_hip_fp32_gemm(model):
                 mod.ops = FP32AccumMatMul()
                 n += 1
     return n
+
+
+def stack_qkv_gemms(model):
+    """Let every attention block of a model run q, k and v as one GEMM over their stacked
+    weights (N = q + k + v outputs) where their operators allow it with the same bits per
+    output column; the parameters then view row ranges of the stack.  Returns the number of
+    attention blocks switched."""
+    n = 0
+    for mod in model.modules():
+        if hasattr(mod, "stack_qkv"):
+            mod.stack_qkv = True
+            n += 1
+    return n

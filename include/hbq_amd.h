@@ -144,10 +144,11 @@ int hbq_gemm_group_partials(const void *A, const void *B, void *P, int64_t M, in
 
 /* No reference counterpart: the non-finite test of a GEMM output
  * (torch.isfinite(y).all() after the linear, src/module.py:51-66) without a host
- * synchronization.  Sets the device int *flag to 1 if any of the n elements of
- * x (16-byte aligned) is NaN or +-inf; leaves it unchanged otherwise.  Writers
- * only ever store 1, so one flag may collect several calls. */
-int hbq_flag_nonfinite(const void *x, int64_t n, int dtype, int *flag, void *stream);
+ * synchronization.  x is rows x cols elements with row stride ld (elements), as a
+ * column slice of a wider output is.  Sets the device int *flag to 1 if any
+ * element is NaN or +-inf; leaves it unchanged otherwise.  Writers only ever
+ * store 1, so one flag may collect several calls. */
+int hbq_flag_nonfinite(const void *x, int64_t rows, int64_t cols, int64_t ld, int dtype, int *flag, void *stream);
 
 /* No reference counterpart: dst[cols, rows] = src[rows, cols]^T for 16-bit
  * elements.  The blockquant_ext front end uses it to hand a B[K,N] operand to

@@ -102,12 +102,35 @@ def test_flag_nonfinite(gpu, dt):
             base[1] = torch.finfo(dt).tiny / 4   # subnormal
             base[2] = -0.0
         flag = torch.zeros(1, dtype=torch.int32, device=gpu)
-        _lib.check(L.hbq_flag_nonfinite(_lib.ptr(base), n, _lib.DTYPE_CODE[dt], _lib.ptr(flag), _lib.stream_of(base)))
+        _lib.check(L.hbq_flag_nonfinite(_lib.ptr(base), 1, n, n, _lib.DTYPE_CODE[dt], _lib.ptr(flag),
+                                        _lib.stream_of(base)))
         assert int(flag.item()) == 0, n
         for pos in sorted({0, n // 2, n - 1}):
             for bad in (float("nan"), float("inf"), -float("inf")):
                 x = base.clone()
                 x[pos] = bad
                 flag.zero_()
-                _lib.check(L.hbq_flag_nonfinite(_lib.ptr(x), n, _lib.DTYPE_CODE[dt], _lib.ptr(flag), _lib.stream_of(x)))
+                _lib.check(L.hbq_flag_nonfinite(_lib.ptr(x), 1, n, n, _lib.DTYPE_CODE[dt], _lib.ptr(flag),
+                                                _lib.stream_of(x)))
                 assert int(flag.item()) == 1, (n, pos, bad)
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.float32])
+def test_flag_nonfinite_column_slice(gpu, dt):
+    """A column slice of a wider output (row stride > cols): only its own columns count."""
+    from hbq_amd import _lib
+    L = _lib.lib()
+    y = torch.randn(64, 96, device=gpu).to(dt)
+    y[5, 90] = float("nan")                      # outside the slice [:, 8:72]
+    flag = torch.zeros(1, dtype=torch.int32, device=gpu)
+    for lo, hi, expect in ((8, 72, 0), (8, 91, 1), (3, 8, 0), (3, 9, 0)):
+        sl = y[:, lo:hi]
+        flag.zero_()
+        _lib.check(L.hbq_flag_nonfinite(_lib.ptr(sl), sl.shape[0], sl.shape[1], sl.stride(0),
+                                        _lib.DTYPE_CODE[dt], _lib.ptr(flag), _lib.stream_of(sl)))
+        assert int(flag.item()) == expect, (lo, hi)
+    y[63, 8] = -float("inf")
+    flag.zero_()
+    sl = y[:, 8:72]
+    _lib.check(L.hbq_flag_nonfinite(_lib.ptr(sl), 64, 64, 96, _lib.DTYPE_CODE[dt], _lib.ptr(flag), _lib.stream_of(sl)))
+    assert int(flag.item()) == 1

@@ -133,3 +133,71 @@ def test_hip_fp32_gemm_linears(gpu):
     rel = ((a - b).norm() / a.norm()).item()
     print(f"hip fp32 gemm vs F.linear: normwise rel {rel:.2e}", flush=True)
     assert rel < 2e-2
+
+
+def test_stacked_weight_views_cpu():
+    """The stack holds the weights as consecutive row ranges; parameters view it (in-place
+    updates reach it); a replaced weight makes the next call build it again."""
+    from hbq_amd.module import _stacked_weight
+    torch.manual_seed(1)
+    mods = [_QBaseLinear(32, n, bias=False) for n in (48, 16, 16)]
+    ref = [m.weight.detach().clone() for m in mods]
+    W = _stacked_weight(mods)
+    assert W.shape == (80, 32) and torch.equal(W, torch.cat(ref))
+    assert all(m.weight.data_ptr() == W[o:].data_ptr() for m, o in zip(mods, (0, 48, 64)))
+    assert _stacked_weight(mods) is W
+    with torch.no_grad():
+        mods[1].weight[3].fill_(7.0)            # in place: lands in the stack
+    assert torch.equal(W[51], torch.full((32,), 7.0)) and _stacked_weight(mods) is W
+    new = torch.randn(16, 32)
+    mods[2].weight.data = new.clone()           # replaced: built again with the new rows
+    W2 = _stacked_weight(mods)
+    assert W2 is not W and torch.equal(W2[64:], new) and torch.equal(W2[48:64], mods[1].weight)
+    assert mods[2].weight.data_ptr() == W2[64:].data_ptr()
+
+
+def test_fusable_rules_cpu():
+    """Stacking needs one HIP operator type and settings, no bias and psum blocks that do not
+    straddle two linears; a CPU weight is never stacked."""
+    from hbq_amd.module import _fusable
+    from hbq_amd.ops import FP16AccumMatMul
+    mods = [_QBaseLinear(32, n, bias=False, ops=FP16AccumMatMul(64, 32)) for n in (64, 32)]
+    for m in mods:
+        m.half()
+    assert not _fusable(mods)                   # CPU weights
+    assert not _fusable([_QBaseLinear(32, 64, bias=False), _QBaseLinear(32, 64, bias=False)])   # F.linear
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ops", ["fp32", "fp16", "grouped", "mxint8"])
+def test_stacked_qkv_bit_identical(gpu, ops):
+    """A prefill with q, k and v as one GEMM over the stacked weights gives the same bits as
+    three GEMMs, for every HIP accumulation mode; after a weight is replaced the stack follows."""
+    from hbq_amd.module import _fusable
+    from hbq_amd.ops import FP16AccumMatMul, FP32AccumMatMul, stack_qkv_gemms
+    print(f"stacked qkv {ops}", flush=True)
+    make = {"fp32": FP32AccumMatMul, "fp16": FP16AccumMatMul, "grouped": lambda: FP16AccumMatMul(64),
+            "mxint8": lambda: FP16AccumMatMul(64, 16)}[ops]
+    m = LlamaForCausalLM(TINY).random_init_(seed=8).half().to(gpu)
+    p = PTQ(hbq_cfg(kv=True), m)
+    p.inject_quantizers()
+    for mod in m.modules():
+        if isinstance(mod, _QBaseLinear) and mod is not m.lm_head:
+            mod.ops = make()
+    p.static_quant_wgt()
+    ids = torch.randint(0, TINY.vocab_size, (1, 96), device=gpu, generator=torch.Generator(device=gpu).manual_seed(8))
+    a = m.layers[0].self_attn
+    with torch.no_grad():
+        sep = m(ids)
+        assert stack_qkv_gemms(m) == TINY.num_hidden_layers
+        assert _fusable((a.q_proj, a.k_proj, a.v_proj))
+        st = m(ids)
+        assert a.q_proj.weight.data_ptr() == a.q_proj.__dict__["_hbq_stack"].data_ptr()
+        assert torch.equal(sep.view(torch.int16), st.view(torch.int16))
+        a.v_proj.weight.data = a.v_proj.weight.detach().flip(0).contiguous()
+        st2 = m(ids)
+        for layer in m.layers:
+            layer.self_attn.stack_qkv = False
+        sep2 = m(ids)
+    assert torch.equal(sep2.view(torch.int16), st2.view(torch.int16))
+    assert not torch.equal(st.view(torch.int16), st2.view(torch.int16))
