@@ -300,6 +300,39 @@ __global__ __launch_bounds__(kThreads) void nonfinite_kernel(const uint8_t* __re
     if (bad) *flag = 1;
 }
 
+namespace hbq {
+
+int hbq_l2_table(HbqParams& p, int& S, int l2_sc_bit, int l2_scheme, int dtype) {
+    if (l2_sc_bit < 0 || l2_sc_bit > 3)
+        return hbq_fail(HBQ_ERR_UNSUPPORTED, "l2_sc_bit %d not supported on the GPU path (0..3)", l2_sc_bit);
+    p.J = 1 << l2_sc_bit;
+    S = 1;
+    // L2 candidate tables (src/quantizer.py:745-770), each entry rounded to T
+    for (int r = 0; r < p.J; ++r) {
+        double rr = r, b1 = 1 << l2_sc_bit, b2 = 1 << (l2_sc_bit + 1), b3 = 1 << (l2_sc_bit + 2);
+        double fp = 1 + rr / b1, fp10 = 1 + rr / b2;
+        double v;
+        switch (l2_scheme) {
+            case 0: v = ldexp(1.0, r); break;
+            case 1: v = rr + 1; break;
+            case 2: v = 1 + rr / 2; break;
+            case 3: v = fp; break;
+            case 4: v = 1 + (rr + 1) / b1; break;
+            case 5: v = fp10; break;
+            case 6: v = 1 + rr / b3; break;
+            case 7: v = fp; S = 2; break;
+            default: return hbq_fail(HBQ_ERR_INVALID, "Invalid L2 scheme code %d", l2_scheme);
+        }
+        p.l2[r][0] = round_host(v, dtype);
+        p.l2[r][1] = round_host(l2_scheme == 7 ? fp10 : v, dtype);
+        p.rl2[r][0] = 1.0f / p.l2[r][0];
+        p.rl2[r][1] = 1.0f / p.l2[r][1];
+    }
+    return 0;
+}
+
+}  // namespace hbq
+
 extern "C" {
 
 // Test hook: 1 routes every HBQ and MXFP / NVFP call to the generic kernels (so both can be checked).
@@ -366,30 +399,9 @@ int hbq_hbq_qdq(const void* x, void* y, void* l1_scale, void* l2_index, void* sc
     if (int rc = geometry(g, x, y, codes, rows, cols, block_size, esize)) return rc;
     if (l2_block_size > block_size) return hbq_fail(HBQ_ERR_INVALID, "l2_block_size larger than block_size");
     HbqParams p{};
-    p.J = 1 << l2_sc_bit;
-    // L2 candidate tables (src/quantizer.py:745-770), each entry rounded to T
-    const int J = p.J;
     int S = 1;
-    for (int r = 0; r < J; ++r) {
-        double rr = r, b1 = 1 << l2_sc_bit, b2 = 1 << (l2_sc_bit + 1), b3 = 1 << (l2_sc_bit + 2);
-        double fp = 1 + rr / b1, fp10 = 1 + rr / b2;
-        double v;
-        switch (l2_scheme) {
-            case 0: v = ldexp(1.0, r); break;
-            case 1: v = rr + 1; break;
-            case 2: v = 1 + rr / 2; break;
-            case 3: v = fp; break;
-            case 4: v = 1 + (rr + 1) / b1; break;
-            case 5: v = fp10; break;
-            case 6: v = 1 + rr / b3; break;
-            case 7: v = fp; S = 2; break;
-            default: return hbq_fail(HBQ_ERR_INVALID, "Invalid L2 scheme code %d", l2_scheme);
-        }
-        p.l2[r][0] = round_host(v, dtype);
-        p.l2[r][1] = round_host(l2_scheme == 7 ? fp10 : v, dtype);
-        p.rl2[r][0] = 1.0f / p.l2[r][0];
-        p.rl2[r][1] = 1.0f / p.l2[r][1];
-    }
+    if (int rc = hbq_l2_table(p, S, l2_sc_bit, l2_scheme, dtype)) return rc;
+    const int J = p.J;
     float elemax = round_host(max_norm_h(ebit, mbit), dtype);
     for (int s = 0; s < S; ++s) {
         float m = p.l2[0][s];

@@ -213,6 +213,10 @@ struct HbqParams {
     ScaleFmt sf;                 // E5M3 L1 scale format
 };
 
+// Host: the L2 candidate factors of a scheme (HBQ_L2_* code) rounded to the
+// dtype, and S (2 for Mix, else 1); 0 or an HBQ_ERR_* code.
+int hbq_l2_table(HbqParams& p, int& S, int l2_sc_bit, int l2_scheme, int dtype);
+
 // v replaces best (torch.argmin order: NaN is the smallest, the first minimum wins):
 // v < best, or v NaN and best not.  !(v >= best) is v < best or either NaN.
 __device__ __forceinline__ bool better(float v, float best) { return !(v >= best) & (best == best); }

@@ -95,6 +95,8 @@ def _fusable(mods):
     o = mods[0].ops
     if type(o) not in (FP16AccumMatMul, FP32AccumMatMul):
         return False
+    if any("packed_weight" in m.__dict__ for m in mods):
+        return False
     w0 = mods[0].weight
     for m in mods:
         if type(m.ops) is not type(o) or any(getattr(m.ops, k, None) != getattr(o, k, None)
@@ -166,12 +168,22 @@ class _QBaseLinear(nn.Linear):
         # the weight was quantized in place before inference (src/ptq.py:338-358)
         return self.forward_quantized(self.aq(x))
 
+    def gemm_weight(self) -> torch.Tensor:
+        """The weight the GEMM reads: the parameter, or for a packed weight
+        (hbq_amd.packed.pack_linear_weights) its decoded fake-quantized values."""
+        p = self.__dict__.get("packed_weight")
+        if p is None:
+            return self.weight
+        from .packed import decoded_weight
+        return decoded_weight(p)
+
     def forward_quantized(self, xq: torch.Tensor) -> torch.Tensor:
         """forward() on an input already quantized by a quantizer equal to self.aq."""
+        w = self.gemm_weight()
         if self.ops is None:
-            y = F.linear(xq, self.weight, self.bias)
+            y = F.linear(xq, w, self.bias)
         else:
-            y = self.ops(xq, self.weight, self.bias)
+            y = self.ops(xq, w, self.bias)
         self._check_finite(y)
         return self.yq(y)
 

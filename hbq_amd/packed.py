@@ -1,0 +1,142 @@
+"""Packed HBQ tensors and linears whose weights stay packed in HBM.
+
+The reference keeps fake-quantized fp16 weights (src/ptq.py:338-358); the HBQ
+hardware emits the same quantization as bit fields: E2Mm element codes, an E5M3
+L1 scale byte per block, L2 indices and a scheme bit
+(hardware/HBQ_accelerator/hbq_e_quantizer/top.sv:14-45).  `pack` stores a
+tensor in that form (0.54 B per element for HBQ-A weights instead of 2), and
+`unpack` decodes it on the GPU to exactly the fake-quantized values, so a GEMM on
+the decoded weight gives the same bits as one on the fake-quantized weight.
+
+`pack_linear_weights` quantizes a model's linear weights into packed form and
+frees the fp16 copies; each forward decodes the weight into a scratch buffer shared
+by all layers of that shape, right before its GEMM (`_QBaseLinear.forward_quantized`).
+"""
+from dataclasses import dataclass
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from .quantizer import HBQQuantizer
+
+_SCHEMES = HBQQuantizer.L2_SCHEME
+
+
+def packed_strides(cols, block_size, mbit, l2_block_size, l2_sc_bit, l2_scheme):
+    """Row strides in bytes of the four packed strings (codes, l1, l2, scheme; 0 if absent)."""
+    import ctypes
+    out = (ctypes.c_int64 * 4)()
+    _lib.check(_lib.lib().hbq_hbq_packed_strides(cols, block_size, mbit, l2_block_size, l2_sc_bit,
+                                                 _SCHEMES.index(l2_scheme), ctypes.addressof(out)), ValueError)
+    return tuple(out)
+
+
+@dataclass
+class PackedHBQ:
+    """An HBQ-quantized tensor as bit fields (rows = all leading dims, blocks along the last)."""
+    codes: torch.Tensor                 # uint8 [rows, cols * (mbit + 3) / 8]
+    l1: torch.Tensor                    # uint8 [rows, cols / block_size], E5M3 bytes
+    l2: Optional[torch.Tensor]          # uint8 [rows, ceil(nsub * l2_sc_bit / 8)] or None
+    scheme: Optional[torch.Tensor]      # uint8 [rows, ceil(nblk / 8)] (Mix) or None
+    shape: Tuple[int, ...]
+    dtype: torch.dtype
+    block_size: int
+    mbit: int
+    l2_block_size: int
+    l2_sc_bit: int
+    l2_scheme: str
+
+    @property
+    def nbytes(self) -> int:
+        return sum(t.numel() for t in (self.codes, self.l1, self.l2, self.scheme) if t is not None)
+
+    def unpack(self, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        return unpack(self, out)
+
+
+def pack(quantizer: HBQQuantizer, x: torch.Tensor) -> PackedHBQ:
+    """Quantize x with an HBQQuantizer (as quantizer.q(x) does) and pack the result.
+    The last dimension must be a multiple of the block size (and of 8)."""
+    if not isinstance(quantizer, HBQQuantizer):
+        raise TypeError("pack needs an HBQQuantizer")
+    _lib.require_gpu(x, "pack")
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    st = packed_strides(cols, quantizer.block_size, quantizer.mbit, quantizer.l2_block_size, quantizer.l2_sc_bit,
+                        quantizer.l2_scheme)
+    qo = quantizer.quantize(x)
+    dev = x.device
+    pc = torch.empty((rows, st[0]), dtype=torch.uint8, device=dev)
+    pl1 = torch.empty((rows, st[1]), dtype=torch.uint8, device=dev)
+    pl2 = torch.empty((rows, st[2]), dtype=torch.uint8, device=dev) if st[2] else None
+    ps = torch.empty((rows, st[3]), dtype=torch.uint8, device=dev) if st[3] else None
+    if rows:
+        _lib.check(_lib.lib().hbq_hbq_pack(
+            _lib.ptr(qo.codes), _lib.ptr(qo.scales), _lib.ptr(qo.l2_index), _lib.ptr(qo.scheme), _lib.ptr(pc),
+            _lib.ptr(pl1), _lib.ptr(pl2), _lib.ptr(ps), rows, cols, _lib.DTYPE_CODE[x.dtype], quantizer.block_size,
+            quantizer.mbit, quantizer.l2_block_size, quantizer.l2_sc_bit, _SCHEMES.index(quantizer.l2_scheme),
+            _lib.stream_of(x)), ValueError)
+    return PackedHBQ(pc, pl1, pl2, ps, tuple(x.shape), x.dtype, quantizer.block_size, quantizer.mbit,
+                     quantizer.l2_block_size, quantizer.l2_sc_bit, quantizer.l2_scheme)
+
+
+def unpack(p: PackedHBQ, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Decode a packed tensor to its fake-quantized values (the quantizer's q(x), bit for bit)."""
+    cols = p.shape[-1]
+    rows = p.codes.shape[0]
+    if out is None:
+        out = torch.empty(p.shape, dtype=p.dtype, device=p.codes.device)
+    elif out.shape != torch.Size(p.shape) or out.dtype != p.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor of the packed shape and dtype")
+    if rows and cols:
+        _lib.check(_lib.lib().hbq_hbq_unpack(
+            _lib.ptr(p.codes), _lib.ptr(p.l1), _lib.ptr(p.l2), _lib.ptr(p.scheme), _lib.ptr(out), rows, cols,
+            _lib.DTYPE_CODE[p.dtype], p.block_size, p.mbit, p.l2_block_size, p.l2_sc_bit,
+            _SCHEMES.index(p.l2_scheme), _lib.stream_of(out)), ValueError)
+    return out
+
+
+# ---- linears with packed weights ---------------------------------------------------------------
+
+_SCRATCH = {}
+
+
+def _scratch(shape, dtype, device):
+    """One decode buffer per (shape, dtype, device), reused by every layer of that shape:
+    layers run one after another on one stream, so a buffer is free again once the GEMM
+    that read it has been issued after it."""
+    key = (tuple(shape), dtype, device)
+    buf = _SCRATCH.get(key)
+    if buf is None:
+        buf = _SCRATCH[key] = torch.empty(shape, dtype=dtype, device=device)
+    return buf
+
+
+def decoded_weight(p: PackedHBQ) -> torch.Tensor:
+    """The fake-quantized weight of a packed linear, decoded into the shared scratch buffer
+    of its shape (valid until the next decode of that shape on the stream)."""
+    return unpack(p, _scratch(p.shape, p.dtype, p.codes.device))
+
+
+def pack_linear_weights(model) -> int:
+    """Quantize every _QBaseLinear weight with its HBQ weight quantizer into packed form
+    (instead of PTQ.static_quant_wgt's in-place fake quantization, src/ptq.py:338-358: the
+    weights must not be quantized yet) and free the fp16 weight; forwards decode it into a
+    shared scratch buffer before the GEMM, which then sees exactly the fake-quantized weight.
+    The packed strings are plain attributes: move the model before packing.  Returns the
+    number of linears packed."""
+    from .module import _QBaseLinear
+    n = 0
+    for mod in model.modules():
+        if not isinstance(mod, _QBaseLinear) or not isinstance(mod.wq, HBQQuantizer):
+            continue
+        w = mod.weight
+        if w.shape[-1] % mod.wq.block_size or not w.is_cuda:
+            continue
+        with torch.no_grad():
+            mod.packed_weight = pack(mod.wq, w.detach())
+        mod._parameters["weight"] = torch.nn.Parameter(torch.empty(0, dtype=w.dtype, device=w.device),
+                                                       requires_grad=False)
+        n += 1
+    return n

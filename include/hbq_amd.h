@@ -90,6 +90,37 @@ int hbq_hbq_qdq(const void *x, void *y, void *l1_scale, void *l2_index, void *sc
                 void *stream);
 
 /*
+ * Packed HBQ tensors (no reference counterpart in src/: the bit layout of the
+ * HBQ hardware quantizer's outputs, hardware/HBQ_accelerator/hbq_e_quantizer/
+ * top.sv:14-45, and of the MAC test vectors, hardware/BQ/MAC_WXAY/tb_WXAY.sv:68-110).
+ * For [rows, cols] with cols % block_size == 0, block_size % 8 == 0 and mbit in
+ * 1..3, each row packs into four byte strings:
+ *   pcodes  cols fields of mbit + 3 bits (the element codes above), element i at
+ *           bits [(mbit+3) i, (mbit+3)(i+1)) of the row's little-endian bit string
+ *   pl1     one E5M3 byte per block: exponent field (bias 15) << 3 | mantissa,
+ *           the bits [14:7] of the scale as fp16; 0xFF for a non-finite scale
+ *   pl2     l2_sc_bit bits per sub-block, LSB first (NULL when l2_sc_bit == 0)
+ *   pscheme one bit per block, LSB first (Mix only, else NULL)
+ * hbq_hbq_packed_strides writes the four row strides in bytes (0 for an absent string).
+ */
+int hbq_hbq_packed_strides(int64_t cols, int block_size, int mbit, int l2_block_size, int l2_sc_bit,
+                           int l2_scheme, int64_t *strides);
+
+/* Packs hbq_hbq_qdq's codes, l1_scale, l2_index and scheme outputs (same
+ * geometry and configuration) into the strings above.  Code buffers 8-byte aligned. */
+int hbq_hbq_pack(const void *codes, const void *l1_scale, const void *l2_index, const void *scheme, void *pcodes,
+                 void *pl1, void *pl2, void *pscheme, int64_t rows, int64_t cols, int dtype, int block_size,
+                 int mbit, int l2_block_size, int l2_sc_bit, int l2_scheme, void *stream);
+
+/* Decodes packed strings to y [rows, cols] in dtype: per element
+ * R(R(level * l2[j][s]) * l1) with the code's sign, the dequantization of
+ * HBQQuantizer.q (src/quantizer.py:790-796), so unpack(pack(q)) equals
+ * hbq_hbq_qdq's y bit for bit.  y 16-byte aligned. */
+int hbq_hbq_unpack(const void *pcodes, const void *pl1, const void *pl2, const void *pscheme, void *y, int64_t rows,
+                   int64_t cols, int dtype, int block_size, int mbit, int l2_block_size, int l2_sc_bit,
+                   int l2_scheme, void *stream);
+
+/*
  * Elementwise E2Mm quantization with subnormals.
  * Replaces the callable returned by make_fp_quant(ebit, mbit) (src/quantizer.py:187-257)
  * and served by GLOBAL_FP_QUANT_CACHE (src/quantizer.py:38-65).  codes optional, one byte each.
