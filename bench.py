@@ -231,6 +231,29 @@ HBQ_A_KV = {
 }
 
 
+def packed_extra(dev, iters=20):
+    """Packed HBQ-A weight of the gate/up shape (14336 x 4096 fp16, N(0, 0.02)): quantize + pack,
+    and the decode back to the fake-quantized fp16 weight that a GEMM reads."""
+    from hbq_amd.packed import pack, unpack
+    from hbq_amd.quantizer import HBQQuantizer
+    g = torch.Generator(device=dev).manual_seed(14)
+    W = (torch.randn(14336, 4096, device=dev, generator=g) * 0.02).half()
+    q = HBQQuantizer(128, 2, 1, 5, 3, 8, 2, "Mix")
+    p = pack(q, W)
+    out = torch.empty_like(W)
+    for _ in range(3):
+        unpack(p, out)
+    t_un = HipTimer().run(lambda: unpack(p, out), iters)
+    t_pk = HipTimer().run(lambda: pack(q, W), 5)
+    n = W.numel()
+    un_bytes = p.nbytes + 2 * n
+    return {"packed_wgt_bytes_per_elem": round(p.nbytes / n, 4),
+            "packed_wgt_unpack_us": round(t_un * 1e6, 1),
+            "packed_wgt_unpack_GBs": round(un_bytes / t_un / 1e9, 1),
+            "packed_wgt_unpack_frac": round(un_bytes / t_un / 1e9 / HBM_PEAK_GBS, 4),
+            "packed_wgt_quantize_pack_ms": round(t_pk * 1e3, 3)}
+
+
 def prefill_extra(dev, T=2048, iters=3):
     """one prefill of T tokens through Llama-3-8B (32 layers, random N(0, 0.02)
     weights, fp16) with the HBQ-A + KV quantization points; weights quantized once beforehand."""
@@ -372,6 +395,7 @@ def main():
             t = HipTimer().run(s4, 100)
             extra[f"{name}_fp16_GBs"] = round(n * mx_bytes_per_elem(c) / t / 1e9, 1)
             extra[f"{name}_fp16_frac"] = round(n * mx_bytes_per_elem(c) / t / 1e9 / HBM_PEAK_GBS, 4)
+        extra.update(packed_extra(dev))
         if not args.quant_only:
             extra.update(config0_extra(dev))
             extra.update(gemm_extra(dev))

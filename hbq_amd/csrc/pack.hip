@@ -16,7 +16,11 @@
 // (src/quantizer.py:790-796) from the level q of each code, so unpack(pack(...))
 // reproduces the quantizer's output bit for bit.
 #include <hip/hip_runtime.h>
+#include <math.h>
 #include <stdint.h>
+#include <string.h>
+
+#include <type_traits>
 
 #include "hbq_capi_internal.h"
 #include "quant_common.h"
@@ -24,8 +28,10 @@
 namespace hbq {
 namespace {
 
+// R_T(level value * l2[j][s]) for every scheme s, candidate j and level (block
+// independent), rounded on the host; indexed [(s * 8 + j) * 32 + level]
 struct UnpackParams {
-    float l2[kMaxJ][2];   // L2 factors per candidate and scheme, rounded to T
+    float qs[2 * kMaxJ * 32];
 };
 
 // E5M3 byte of a scale held in T (0xFF if it is not a finite E5M3 value)
@@ -48,14 +54,6 @@ __device__ __forceinline__ float e5m3_value(uint32_t byte) {
     if (e == 31) return __builtin_nanf("");
     if (e == 0) return (float)m * 0x1p-17f;
     return bits2f(((e - 15u + 127u) << 23) | (m << 20));
-}
-
-// magnitude of an E2Mm level (exponent field 0 = subnormal)
-template <int M>
-__device__ __forceinline__ float level_mag(uint32_t level) {
-    const uint32_t e = level >> M, m = level & ((1u << M) - 1u);
-    const float frac = (float)m * (1.0f / (float)(1 << M));
-    return e == 0 ? frac : (1.0f + frac) * (float)(1u << (e - 1));
 }
 
 // thread = (row, 8 elements): quantizer codes -> (M+3)-bit fields
@@ -116,55 +114,110 @@ __device__ __forceinline__ uint32_t get_bits(const uint8_t* __restrict__ row, in
     return (v >> (pos & 7)) & ((1u << w) - 1u);
 }
 
-// thread = (row, 8 elements): fields -> d = R(R(q l2[j][s]) l1) with the code's sign
+// Decode: a workgroup copies the block-independent magnitudes R(level * l2[j][s])
+// to LDS; a thread decodes 8 consecutive elements of one row (one block, at most
+// two sub-blocks): per element one LDS read, then d = R(m * l1) and the code's sign.
+// fp16 multiplies pairs with v_pk_mul_f16 (one rounding of the exact product of
+// two fp16 values, as R16(m * l1) needs); bf16 multiplies in fp32 and rounds a
+// pair with one v_cvt_pk_bf16_f32.
 template <class T, int M>
 __global__ __launch_bounds__(kThreads) void unpack_kernel(const uint8_t* __restrict__ pc, const uint8_t* __restrict__ pl1,
                                                           const uint8_t* __restrict__ pl2, const uint8_t* __restrict__ ps,
                                                           typename T::storage* __restrict__ y, int64_t rows, int64_t cols,
                                                           int block, int l2b, int l2bits, int S, UnpackParams p) {
     constexpr int W = M + 3;
-    const int64_t groups = cols / 8;
-    const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    if (t >= rows * groups) return;
-    const int64_t r = t / groups, g = t - r * groups;
-    const int64_t c0 = g * 8;
-    const int64_t nblk = cols / block, blk = c0 / block;
-    const float l1 = e5m3_value(pl1[r * nblk + blk]);
-    int s = 0;
-    if (S == 2) s = (ps[r * ((nblk + 7) / 8) + (blk >> 3)] >> (blk & 7)) & 1;
-    const int64_t l2_row = (cols / l2b * l2bits + 7) / 8;
-    const uint8_t* l2r = pl2 + r * l2_row;
+    constexpr int L = 1 << (M + 2);
+    constexpr bool H = sizeof(typename T::storage) == 2 && T::dt == kF16;
+    using E = typename std::conditional<H, _Float16, float>::type;
+    __shared__ E tab[2 * kMaxJ * L];
+    for (int i = threadIdx.x; i < 2 * kMaxJ * L; i += kThreads) tab[i] = (E)p.qs[(i / L) * 32 + (i % L)];
+    __syncthreads();
 
-    uint64_t acc = 0;
-    const uint8_t* src = pc + r * (cols * W / 8) + g * W;
-    if constexpr (M == 1) {
-        acc = *reinterpret_cast<const uint32_t*>(src);
-    } else {
+    const int64_t groups = cols / 8;
+    const int64_t g = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (g >= groups) return;
+    const int64_t nblk = cols / block;
+    const int64_t l2_row = (cols / l2b * l2bits + 7) / 8;
+    const int64_t c0 = g * 8, blk = c0 / block;
+#pragma unroll 2
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        const float l1 = e5m3_value(pl1[r * nblk + blk]);
+        const int s = S == 2 ? (ps[r * ((nblk + 7) / 8) + (blk >> 3)] >> (blk & 7)) & 1 : 0;
+        // candidates of the (one or two) sub-blocks of these 8 elements
+        int j0 = 0, j1 = 0;
+        if (l2bits) {
+            const uint8_t* l2r = pl2 + r * l2_row;
+            j0 = (int)get_bits(l2r, c0 / l2b * l2bits, l2bits, l2_row);
+            j1 = l2b >= 8 ? j0 : (int)get_bits(l2r, (c0 + 4) / l2b * l2bits, l2bits, l2_row);
+        }
+        const E* t0 = tab + (s * kMaxJ + j0) * L;
+        const E* t1 = tab + (s * kMaxJ + j1) * L;
+
+        uint64_t acc = 0;
+        const uint8_t* src = pc + r * (cols * W / 8) + g * W;
+        if constexpr (M == 1) {
+            acc = *reinterpret_cast<const uint32_t*>(src);
+        } else {
 #pragma unroll
-        for (int i = 0; i < W; ++i) acc |= (uint64_t)src[i] << (8 * i);
-    }
-    float out[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const uint32_t code = (uint32_t)(acc >> (W * i)) & ((1u << W) - 1u);
-        const int j = l2bits ? (int)get_bits(l2r, (c0 + i) / l2b * l2bits, l2bits, l2_row) : 0;
-        const float l2 = s ? p.l2[j][1] : p.l2[j][0];
-        const float d = T::round(T::round(level_mag<M>(code & ((1u << (M + 2)) - 1u)) * l2) * l1);
-        out[i] = (code >> (M + 2)) ? -d : d;
-    }
-    typename T::storage* dst = y + r * cols + c0;
-    if constexpr (sizeof(typename T::storage) == 2) {
+            for (int i = 0; i < W; ++i) acc |= (uint64_t)src[i] << (8 * i);
+        }
         uint32_t w[4];
+        if constexpr (H) {
+            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+            const _Float16 l1h = (_Float16)l1;   // an E5M3 value: exact in fp16
 #pragma unroll
-        for (int i = 0; i < 4; ++i) w[i] = (uint32_t)T::store(out[2 * i]) | ((uint32_t)T::store(out[2 * i + 1]) << 16);
-        *reinterpret_cast<u32x4*>(dst) = (u32x4){w[0], w[1], w[2], w[3]};
-    } else {
-        *reinterpret_cast<f32x4*>(dst) = (f32x4){out[0], out[1], out[2], out[3]};
-        *reinterpret_cast<f32x4*>(dst + 4) = (f32x4){out[4], out[5], out[6], out[7]};
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t ca = (uint32_t)(acc >> (W * 2 * k)) & ((1u << W) - 1u);
+                const uint32_t cb = (uint32_t)(acc >> (W * (2 * k + 1))) & ((1u << W) - 1u);
+                const E* tk = k < 2 ? t0 : t1;
+                const h2 m = {tk[ca & (L - 1)], tk[cb & (L - 1)]};
+                const h2 d = m * (h2){l1h, l1h};
+                asm volatile("" : : "v"(d));
+                w[k] = __builtin_bit_cast(uint32_t, d) | ((ca >> (M + 2)) << 15) | ((cb >> (M + 2)) << 31);
+            }
+        } else if constexpr (sizeof(typename T::storage) == 2) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t ca = (uint32_t)(acc >> (W * 2 * k)) & ((1u << W) - 1u);
+                const uint32_t cb = (uint32_t)(acc >> (W * (2 * k + 1))) & ((1u << W) - 1u);
+                const E* tk = k < 2 ? t0 : t1;
+                const bf16x2_t d = __builtin_convertvector((f32x2_t){tk[ca & (L - 1)] * l1, tk[cb & (L - 1)] * l1},
+                                                           bf16x2_t);
+                w[k] = __builtin_bit_cast(uint32_t, d) | ((ca >> (M + 2)) << 15) | ((cb >> (M + 2)) << 31);
+            }
+        }
+        typename T::storage* dst = y + r * cols + c0;
+        if constexpr (sizeof(typename T::storage) == 2) {
+            *reinterpret_cast<u32x4*>(dst) = (u32x4){w[0], w[1], w[2], w[3]};
+        } else {
+            float out[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t c = (uint32_t)(acc >> (W * i)) & ((1u << W) - 1u);
+                const float d = (i < 4 ? t0 : t1)[c & (L - 1)] * l1;
+                out[i] = bits2f(f2bits(d) | ((c >> (M + 2)) << 31));
+            }
+            *reinterpret_cast<f32x4*>(dst) = (f32x4){out[0], out[1], out[2], out[3]};
+            *reinterpret_cast<f32x4*>(dst + 4) = (f32x4){out[4], out[5], out[6], out[7]};
+        }
     }
 }
 
 unsigned grid_for(int64_t n) { return (unsigned)((n + kThreads - 1) / kThreads); }
+
+// round an exactly representable-in-double value to the dtype (RNE), on the host
+float round_to(double v, int dt) {
+    float f = (float)v;   // exact: a level times an L2 factor has few significant bits
+    if (dt == kF16) return (float)(_Float16)f;
+    if (dt == kBF16) {
+        uint32_t x;
+        memcpy(&x, &f, 4);
+        x += 0x7fffu + ((x >> 16) & 1u);
+        x &= 0xffff0000u;
+        memcpy(&f, &x, 4);
+    }
+    return f;
+}
 
 // shared argument checks; fills the row strides
 int check_geometry(int64_t rows, int64_t cols, int dtype, int block, int mbit, int l2b, int l2_sc_bit, int l2_scheme,
@@ -257,11 +310,22 @@ int hbq_hbq_unpack(const void* pcodes, const void* pl1, const void* pl2, const v
     int S = 1;
     if (int rc = hbq_l2_table(hp, S, l2_sc_bit, l2_scheme, dtype)) return rc;
     UnpackParams p{};
-    for (int j = 0; j < kMaxJ; ++j)
-        for (int s = 0; s < 2; ++s) p.l2[j][s] = j < hp.J ? hp.l2[j][s] : 1.f;
+    for (int s = 0; s < 2; ++s)
+        for (int j = 0; j < kMaxJ; ++j)
+            for (int lev = 0; lev < 32; ++lev) {
+                const int e = lev >> mbit, m = lev & ((1 << mbit) - 1);
+                const double lv = e == 0 ? ldexp((double)m, -mbit) : ldexp(1.0 + ldexp((double)m, -mbit), e - 1);
+                const double l2 = j < hp.J ? hp.l2[j][s] : 1.0;
+                p.qs[(s * kMaxJ + j) * 32 + lev] = lev < (4 << mbit) ? round_to(lv * l2, dtype) : 0.f;
+            }
     hipStream_t st = (hipStream_t)stream;
-    const int64_t groups = rows * (cols / 8);
-    const dim3 grid(grid_for(groups));
+    const int64_t groups = cols / 8;
+    if (groups > 0x7fffffffll * kThreads) return hbq_fail(HBQ_ERR_INVALID, "rows too long");
+    // about 2048 workgroups (8 per CU), each walking rows: the LDS table is built once per workgroup
+    const int64_t gx = grid_for(groups);
+    int64_t gy = 2048 / gx;
+    gy = gy < 1 ? 1 : (gy > rows ? rows : (gy > 65535 ? 65535 : gy));
+    const dim3 grid((unsigned)gx, (unsigned)gy);
 #define UNPACK(TT, MM)                                                                                             \
     hipLaunchKernelGGL((unpack_kernel<TT, MM>), grid, dim3(kThreads), 0, st, (const uint8_t*)pcodes,              \
                        (const uint8_t*)pl1, (const uint8_t*)pl2, (const uint8_t*)pscheme, (TT::storage*)y, rows, cols, \
