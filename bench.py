@@ -256,9 +256,12 @@ def packed_extra(dev, iters=20):
 
 def prefill_extra(dev, T=2048, iters=3):
     """one prefill of T tokens through Llama-3-8B (32 layers, random N(0, 0.02)
-    weights, fp16) with the HBQ-A + KV quantization points; weights quantized once beforehand."""
+    weights, fp16) with the HBQ-A + KV quantization points; weights quantized once beforehand.
+    Then the same with the decoder weights packed (hbq_amd.packed), checked for the same logits."""
     from hbq_amd.llama import LlamaConfig, LlamaForCausalLM
+    from hbq_amd.module import _QBaseLinear
     from hbq_amd.ops import stack_qkv_gemms, use_hip_fp32_gemm
+    from hbq_amd.packed import pack_linear_weights
     from hbq_amd.ptq import PTQ
     cfg = LlamaConfig()
     with torch.device(dev):
@@ -283,10 +286,36 @@ def prefill_extra(dev, T=2048, iters=3):
         torch.cuda.synchronize()
     t = (time.perf_counter() - t0) / iters
     assert torch.isfinite(out).all()
-    del m, out
+    w_bytes = sum(mod.weight.numel() * 2 for mod in m.modules() if isinstance(mod, _QBaseLinear) and mod is not m.lm_head)
+    del m
+    torch.cuda.empty_cache()
+
+    # the same model with its decoder weights packed (decoded before each GEMM): same logits
+    with torch.device(dev):
+        m = LlamaForCausalLM(cfg).half()
+    m.random_init_(seed=4)
+    p = PTQ(HBQ_A_KV, m)
+    p.inject_quantizers()
+    use_hip_fp32_gemm(m)
+    stack_qkv_gemms(m)
+    pack_linear_weights(m)
+    pw_bytes = sum(mod.packed_weight.nbytes for mod in m.modules() if "packed_weight" in mod.__dict__)
+    with torch.no_grad():
+        m(ids)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            out2 = m(ids)
+        torch.cuda.synchronize()
+    t_p = (time.perf_counter() - t0) / iters
+    same = bool(torch.equal(out.view(torch.int16), out2.view(torch.int16)))
+    del m, out, out2
     torch.cuda.empty_cache()
     return {"cfg4_prefill_ms": round(t * 1e3, 2), "cfg4_prefill_tokens_per_s": round(T / t, 1),
-            "cfg4_weight_quant_ms": round(t_wq * 1e3, 1)}
+            "cfg4_weight_quant_ms": round(t_wq * 1e3, 1),
+            "cfg4_prefill_packed_ms": round(t_p * 1e3, 2), "cfg4_packed_logits_identical": same,
+            "cfg4_decoder_weight_GB_fp16": round(w_bytes / 1e9, 2),
+            "cfg4_decoder_weight_GB_packed": round(pw_bytes / 1e9, 2)}
 
 
 def cpu_model():

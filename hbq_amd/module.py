@@ -95,26 +95,40 @@ def _fusable(mods):
     o = mods[0].ops
     if type(o) not in (FP16AccumMatMul, FP32AccumMatMul):
         return False
-    if any("packed_weight" in m.__dict__ for m in mods):
+    packed = ["packed_weight" in m.__dict__ for m in mods]
+    if any(packed) and not all(packed):
         return False
-    w0 = mods[0].weight
+    w0 = _weight_meta(mods[0])
     for m in mods:
         if type(m.ops) is not type(o) or any(getattr(m.ops, k, None) != getattr(o, k, None)
                                              for k in ("group_size", "quant_block_size")):
             return False
-        w = m.weight
-        if m.bias is not None or w.dtype != torch.float16 or not w.is_cuda or w.device != w0.device \
-                or w.dim() != 2 or w.shape[1] != w0.shape[1] or not w.is_contiguous():
+        shape, dtype, device, contiguous = _weight_meta(m)
+        if m.bias is not None or dtype != torch.float16 or device.type != "cuda" or device != w0[2] \
+                or len(shape) != 2 or shape[1] != w0[0][1] or not contiguous:
             return False
     qb = getattr(o, "quant_block_size", None)
     return qb is None or all(m.out_features % qb == 0 for m in mods[:-1])
+
+
+def _weight_meta(m):
+    """(shape, dtype, device, contiguous) of the weight the GEMM reads (a packed one decodes contiguous)."""
+    p = m.__dict__.get("packed_weight")
+    if p is not None:
+        return tuple(p.shape), p.dtype, p.codes.device, True
+    w = m.weight
+    return tuple(w.shape), w.dtype, w.device, w.is_contiguous()
 
 
 def _stacked_weight(mods):
     """The weights of `mods` as consecutive row ranges of one [sum N, K] tensor.  Built on first
     use by moving each weight into the stack (its parameter then views its rows: no memory is
     added, and in-place updates of a weight land in the stack); built again when a weight has
-    been replaced (assignment to .data, .to(), a new Parameter)."""
+    been replaced (assignment to .data, .to(), a new Parameter).  Packed weights are decoded
+    into consecutive row ranges of a shared scratch stack instead."""
+    if "packed_weight" in mods[0].__dict__:
+        from .packed import decoded_stack
+        return decoded_stack([m.packed_weight for m in mods])
     W = mods[0].__dict__.get("_hbq_stack")
     if W is not None:
         off = 0

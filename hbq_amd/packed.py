@@ -119,6 +119,18 @@ def decoded_weight(p: PackedHBQ) -> torch.Tensor:
     return unpack(p, _scratch(p.shape, p.dtype, p.codes.device))
 
 
+def decoded_stack(ps) -> torch.Tensor:
+    """Packed weights with one K decoded into consecutive row ranges of one shared scratch
+    [sum N, K] buffer (for one GEMM over several linears that read the same input)."""
+    n = sum(p.shape[0] for p in ps)
+    W = _scratch((n, ps[0].shape[1]), ps[0].dtype, ps[0].codes.device)
+    off = 0
+    for p in ps:
+        unpack(p, W[off:off + p.shape[0]])
+        off += p.shape[0]
+    return W
+
+
 def pack_linear_weights(model) -> int:
     """Quantize every _QBaseLinear weight with its HBQ weight quantizer into packed form
     (instead of PTQ.static_quant_wgt's in-place fake quantization, src/ptq.py:338-358: the

@@ -229,4 +229,9 @@ def test_gpu_packed_weights_prefill(gpu, ops):
             p.static_quant_wgt()
         with torch.no_grad():
             outs.append(m(ids))
-    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+            if packed:      # q/k/v decoded into one stacked scratch and run as one GEMM
+                for layer in m.layers:
+                    layer.self_attn.stack_qkv = True
+                outs.append(m(ids))
+    for o in outs[1:]:
+        assert torch.equal(outs[0].view(torch.int16), o.view(torch.int16))
