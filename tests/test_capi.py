@@ -64,3 +64,30 @@ def test_argument_errors_without_gpu(lib):
     rc = L.hbq_mxfp_qdq(ctypes.c_void_p(16), ctypes.c_void_p(16), None, None, 1, 96, 0, 48, 2, 1, 5, 0, 0, 0, 0,
                         0, 1.0, None)
     assert rc == 2 and b"block_size" in L.hbq_last_error()
+
+
+def test_packed_argument_errors_without_gpu(lib):
+    """hbq_hbq_pack / hbq_hbq_unpack / hbq_hbq_flag_nonfinite check their arguments before any HIP call."""
+    from hbq_amd import _lib
+    L = _lib.lib()
+    fake = ctypes.c_void_p(256)            # never dereferenced: the checks fail first
+    # cols not a multiple of the block
+    rc = L.hbq_hbq_pack(fake, fake, fake, fake, fake, fake, fake, fake, 4, 100, 0, 128, 1, 8, 2, 7, None)
+    assert rc == 2 and b"cols % block_size" in L.hbq_last_error()
+    # mbit outside 1..3
+    rc = L.hbq_hbq_unpack(fake, fake, fake, fake, fake, 4, 128, 0, 128, 5, 8, 2, 2, None)
+    assert rc == 2 and b"mbit" in L.hbq_last_error()
+    # Mix needs the scheme strings
+    rc = L.hbq_hbq_unpack(fake, fake, fake, None, ctypes.c_void_p(1024), 4, 128, 0, 128, 1, 8, 2, 7, None)
+    assert rc == 1 and b"scheme" in L.hbq_last_error()
+    # l2_sc_bit > 0 needs the L2 strings
+    rc = L.hbq_hbq_pack(fake, fake, None, None, fake, fake, None, None, 4, 128, 0, 128, 2, 8, 2, 2, None)
+    assert rc == 1 and b"L2" in L.hbq_last_error()
+    # misaligned output
+    rc = L.hbq_hbq_unpack(fake, fake, fake, None, ctypes.c_void_p(1026), 4, 128, 0, 128, 2, 8, 2, 2, None)
+    assert rc == 1 and b"misaligned" in L.hbq_last_error()
+    # empty tensors are a no-op
+    assert L.hbq_hbq_unpack(None, None, None, None, None, 0, 128, 0, 128, 2, 8, 2, 2, None) == 0
+    # non-finite flag: bad stride
+    rc = L.hbq_flag_nonfinite(fake, 4, 8, 4, 0, fake, None)
+    assert rc == 1
