@@ -247,11 +247,30 @@ def packed_extra(dev, iters=20):
     t_pk = HipTimer().run(lambda: pack(q, W), 5)
     n = W.numel()
     un_bytes = p.nbytes + 2 * n
-    return {"packed_wgt_bytes_per_elem": round(p.nbytes / n, 4),
-            "packed_wgt_unpack_us": round(t_un * 1e6, 1),
-            "packed_wgt_unpack_GBs": round(un_bytes / t_un / 1e9, 1),
-            "packed_wgt_unpack_frac": round(un_bytes / t_un / 1e9 / HBM_PEAK_GBS, 4),
-            "packed_wgt_quantize_pack_ms": round(t_pk * 1e3, 3)}
+    out = {"packed_wgt_bytes_per_elem": round(p.nbytes / n, 4),
+           "packed_wgt_unpack_us": round(t_un * 1e6, 1),
+           "packed_wgt_unpack_GBs": round(un_bytes / t_un / 1e9, 1),
+           "packed_wgt_unpack_frac": round(un_bytes / t_un / 1e9 / HBM_PEAK_GBS, 4),
+           "packed_wgt_quantize_pack_ms": round(t_pk * 1e3, 3)}
+    # a decode-sized GEMM (16 rows) on that weight: codes decoded in registers ahead of MFMA, against
+    # the GEMM on the fp16 fake-quantized weight (same bits) and decode + GEMM
+    from hbq_amd import blockquant_ext as ext
+    from hbq_amd.packed import packed_gemm
+    A = (torch.randn(16, 4096, device=dev, generator=g)).half()
+    Wq = unpack(p)
+    for mode, gk, gn, fn in (("fp32", 0, 0, lambda: ext.gemm_fp32_accum_nk(A, Wq)),
+                             ("mxint8", 128, 32, lambda: ext.gemm_blockquant_mxint8_nk(A, Wq, 128, 32))):
+        assert torch.equal(packed_gemm(A, p, mode, gk, gn).view(torch.int16), fn().view(torch.int16))
+        for _ in range(3):
+            packed_gemm(A, p, mode, gk, gn)
+            fn()
+        t_f = HipTimer().run(lambda: packed_gemm(A, p, mode, gk, gn), iters)
+        t_w = HipTimer().run(fn, iters)
+        out[f"decode16_{mode}_packed_us"] = round(t_f * 1e6, 1)
+        out[f"decode16_{mode}_packed_weight_GBs"] = round(p.nbytes / t_f / 1e9, 1)
+        out[f"decode16_{mode}_fp16_weight_us"] = round(t_w * 1e6, 1)
+        out[f"decode16_{mode}_unpack_then_gemm_us"] = round((t_w + t_un) * 1e6, 1)
+    return out
 
 
 def prefill_extra(dev, T=2048, iters=3):

@@ -35,6 +35,7 @@ SIGNATURES = {
     "hbq_hbq_packed_strides": ([_I64, _I, _I, _I, _I, _I, _P], _I),
     "hbq_hbq_pack": ([_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _I, _P], _I),
     "hbq_hbq_unpack": ([_P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _I, _P], _I),
+    "hbq_gemm_packed_w": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
 }
 
 

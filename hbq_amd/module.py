@@ -193,11 +193,17 @@ class _QBaseLinear(nn.Linear):
 
     def forward_quantized(self, xq: torch.Tensor) -> torch.Tensor:
         """forward() on an input already quantized by a quantizer equal to self.aq."""
-        w = self.gemm_weight()
-        if self.ops is None:
-            y = F.linear(xq, w, self.bias)
-        else:
-            y = self.ops(xq, w, self.bias)
+        y = None
+        p = self.__dict__.get("packed_weight")
+        if p is not None and self.ops is not None:
+            from .packed import linear_packed
+            y = linear_packed(xq, p, self.ops, self.bias)   # decode-sized inputs: codes decoded in the GEMM
+        if y is None:
+            w = self.gemm_weight()
+            if self.ops is None:
+                y = F.linear(xq, w, self.bias)
+            else:
+                y = self.ops(xq, w, self.bias)
         self._check_finite(y)
         return self.yq(y)
 

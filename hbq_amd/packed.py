@@ -97,6 +97,64 @@ def unpack(p: PackedHBQ, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     return out
 
 
+# ---- GEMM on a packed weight -------------------------------------------------------------------
+
+ACC_MODES = {"fp32": 0, "grouped": 1, "mxint8": 2, "mxfp8": 3}
+
+
+def packed_gemm_supported(p: PackedHBQ, rows: int) -> bool:
+    """True when hbq_gemm_packed_w takes this weight and row count (E2M1 fp16 weights in blocks
+    of 128, l2 blocks of 8..32 with at most 4 L2 factors below 4, N % 32 == 0, K % 256 == 0, 1..32 rows)."""
+    N, K = p.shape[0], p.shape[-1]
+    return (len(p.shape) == 2 and p.dtype == torch.float16 and p.mbit == 1 and p.block_size == 128
+            and p.l2_block_size in (8, 16, 32) and p.l2_sc_bit <= 2 and p.l2_scheme not in ("PoT", "INT")
+            and 1 <= rows <= 32 and N % 32 == 0 and K % 256 == 0)
+
+
+def packed_gemm(x2d: torch.Tensor, p: PackedHBQ, mode: str = "fp32", group_k: int = 0, group_n: int = 0):
+    """C[M, N] fp16 = x2d[M, K] fp16 @ unpack(p)^T with the accumulation of `mode` (the
+    blockquant_ext op of that name), decoding the codes in registers ahead of MFMA: the same bits
+    as the GEMM on the unpacked weight.  For decode-sized M (1..32 rows)."""
+    _lib.require_gpu(x2d, "packed_gemm")
+    if x2d.dtype != torch.float16 or x2d.dim() != 2 or x2d.shape[1] != p.shape[-1]:
+        raise RuntimeError("x2d must be a 2-D fp16 tensor with the weight's K")
+    x2d = x2d.contiguous()
+    M, K = x2d.shape
+    N = p.shape[0]
+    C = torch.empty((M, N), dtype=torch.float16, device=x2d.device)
+    _lib.check(_lib.lib().hbq_gemm_packed_w(
+        _lib.ptr(x2d), _lib.ptr(p.codes), _lib.ptr(p.l1), _lib.ptr(p.l2), _lib.ptr(p.scheme), _lib.ptr(C), M, N, K,
+        p.block_size, p.mbit, p.l2_block_size, p.l2_sc_bit, _SCHEMES.index(p.l2_scheme), ACC_MODES[mode], group_k,
+        group_n, _lib.stream_of(x2d)))
+    return C
+
+
+def linear_packed(xq: torch.Tensor, p: PackedHBQ, ops, bias=None):
+    """ops(xq, unpack(p), bias) for the HIP accumulation operators, on the packed weight directly when
+    the row count is decode-sized; None when the caller should decode the weight and call ops."""
+    from .ops import FP16AccumMatMul, FP32AccumMatMul
+    rows = xq.numel() // xq.shape[-1] if xq.shape[-1] else 0
+    if not packed_gemm_supported(p, rows) or not xq.is_cuda:
+        return None
+    if isinstance(ops, FP32AccumMatMul):
+        mode, gk, gn = "fp32", 0, 0
+    elif isinstance(ops, FP16AccumMatMul) and ops.quant_block_size is not None:
+        if ops.group_size not in (64, 128) or ops.quant_block_size not in (4, 8, 16, 32):
+            return None     # ops raises the reference's ValueError, or the kernel does not take the group
+        mode, gk, gn = "mxint8", ops.group_size, ops.quant_block_size
+    elif isinstance(ops, FP16AccumMatMul) and ops.group_size in (16, 32, 64, 128):
+        mode, gk, gn = "grouped", ops.group_size, 0
+    else:
+        return None
+    x2d = xq.reshape(-1, xq.shape[-1])
+    if x2d.dtype != torch.float16:
+        x2d = x2d.half()
+    y = packed_gemm(x2d, p, mode, gk, gn)
+    if bias is not None:
+        y = y + bias
+    return y.view(*xq.shape[:-1], -1)
+
+
 # ---- linears with packed weights ---------------------------------------------------------------
 
 _SCRATCH = {}

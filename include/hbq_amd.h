@@ -120,6 +120,24 @@ int hbq_hbq_unpack(const void *pcodes, const void *pl1, const void *pl2, const v
                    int64_t cols, int dtype, int block_size, int mbit, int l2_block_size, int l2_sc_bit,
                    int l2_scheme, void *stream);
 
+/* Accumulation modes of hbq_gemm_packed_w (the blockquant_ext ops they follow) */
+#define HBQ_ACC_FP32 0      /* gemm_fp32_accum */
+#define HBQ_ACC_GROUPED 1   /* gemm_fp16_grouped_accum */
+#define HBQ_ACC_MXINT8 2    /* gemm_blockquant_mxint8 */
+#define HBQ_ACC_MXFP8 3     /* gemm_blockquant_mxfp8 */
+
+/* GEMM on a packed weight for decode-sized M (no counterpart in src/: the
+ * low-bit GEMM the packed format feeds).  C[M,N] fp16 = A[M,K] fp16 x W[N,K]^T
+ * where W is given by hbq_hbq_pack's strings of an fp16 tensor (E2M1 codes,
+ * block 128, l2_block_size 8/16/32, l2_sc_bit <= 2, L2 factors < 4), decoded in
+ * registers ahead of MFMA.  Same bits as unpacking W and running the GEMM of
+ * acc_mode (the blockquant_ext ops of blockquant_ext.cpp:51-72, in W[N,K]
+  * layout).  Limits: 1 <= M <= 32, N % 32 == 0, K % 256 == 0, the group_k /
+ * group_n sets of those ops; A 16-byte, pcodes 4-byte, C 8-byte aligned. */
+int hbq_gemm_packed_w(const void *A, const void *pcodes, const void *pl1, const void *pl2, const void *pscheme,
+                      void *C, int M, int N, int K, int block_size, int mbit, int l2_block_size, int l2_sc_bit,
+                      int l2_scheme, int acc_mode, int group_k, int group_n, void *stream);
+
 /*
  * Elementwise E2Mm quantization with subnormals.
  * Replaces the callable returned by make_fp_quant(ebit, mbit) (src/quantizer.py:187-257)

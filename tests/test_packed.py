@@ -235,3 +235,74 @@ def test_gpu_packed_weights_prefill(gpu, ops):
                 outs.append(m(ids))
     for o in outs[1:]:
         assert torch.equal(outs[0].view(torch.int16), o.view(torch.int16))
+
+
+PACKED_GEMM_CASES = [("fp32", 0, 0), ("grouped", 128, 0), ("grouped", 32, 0), ("grouped", 16, 0),
+                     ("mxint8", 128, 32), ("mxint8", 64, 16), ("mxint8", 256, 4), ("mxfp8", 128, 32),
+                     ("mxfp8", 64, 8)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("wcfg", [(8, 2, "Mix"), (32, 2, "Mix"), (16, 1, "FP-1"), (8, 0, "PoT")])
+@pytest.mark.parametrize("case", PACKED_GEMM_CASES)
+def test_gpu_packed_gemm_bit_identical(gpu, case, wcfg):
+    """The GEMM that decodes the packed weight in registers gives the bits of the blockquant_ext
+    GEMM on the unpacked weight, for 1..32 rows, every accumulation mode and HBQ-A / HBQ-E weights."""
+    from hbq_amd import blockquant_ext as ext
+    from hbq_amd.packed import pack, packed_gemm
+    from hbq_amd.quantizer import HBQQuantizer
+    mode, gk, gn = case
+    l2b, l2s, sch = wcfg
+    print(f"packed gemm {case} {wcfg}", flush=True)
+    K, N = 1024, 416
+    W = synth(N, K, 61, "f16", std=0.02).to(gpu)
+    p = pack(HBQQuantizer(128, 2, 1, 5, 3, l2b, l2s, sch), W)
+    Wq = p.unpack()
+    for M in (1, 5, 16, 32):
+        A = synth(M, K, 62 + M, "f16").to(gpu)
+        ref = {"fp32": lambda: ext.gemm_fp32_accum_nk(A, Wq),
+               "grouped": lambda: ext.gemm_fp16_grouped_accum_nk(A, Wq, gk),
+               "mxint8": lambda: ext.gemm_blockquant_mxint8_nk(A, Wq, gk, gn),
+               "mxfp8": lambda: ext.gemm_blockquant_mxfp8_nk(A, Wq, gk, gn)}[mode]()
+        got = packed_gemm(A, p, mode, gk, gn)
+        assert torch.isfinite(ref.float()).all()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), (M, case, wcfg)
+
+
+@pytest.mark.gpu
+def test_gpu_packed_gemm_decode_step(gpu):
+    """A decode step (4 tokens) through a model with packed weights: the linears take the in-register
+    decode path and the logits equal those of the fake-quantized weights."""
+    from hbq_amd.llama import LlamaConfig, LlamaForCausalLM
+    from hbq_amd.module import _QBaseLinear
+    from hbq_amd.ops import FP16AccumMatMul
+    from hbq_amd import packed as PKD
+    from hbq_amd.packed import pack_linear_weights
+    from hbq_amd.ptq import PTQ
+    from test_ptq import hbq_cfg
+    print("packed decode step", flush=True)
+    tiny = LlamaConfig(hidden_size=512, intermediate_size=1024, num_hidden_layers=2, num_attention_heads=4,
+                       num_key_value_heads=2, vocab_size=1000)
+    ids = torch.randint(0, 1000, (1, 4), device=gpu, generator=torch.Generator(device=gpu).manual_seed(5))
+    outs = []
+    calls = []
+    orig = PKD.packed_gemm
+    for packed in (False, True):
+        m = LlamaForCausalLM(tiny).random_init_(seed=10).half().to(gpu)
+        p = PTQ(hbq_cfg(kv=True), m)
+        p.inject_quantizers()
+        for mod in m.modules():
+            if isinstance(mod, _QBaseLinear) and mod is not m.lm_head:
+                mod.ops = FP16AccumMatMul(128, 32)
+        if packed:
+            pack_linear_weights(m)
+            PKD.packed_gemm = lambda *a, **k: (calls.append(1), orig(*a, **k))[1]
+        else:
+            p.static_quant_wgt()
+        try:
+            with torch.no_grad():
+                outs.append(m(ids))
+        finally:
+            PKD.packed_gemm = orig
+    assert len(calls) == 2 * 7
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
