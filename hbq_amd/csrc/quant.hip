@@ -333,6 +333,38 @@ int hbq_l2_table(HbqParams& p, int& S, int l2_sc_bit, int l2_scheme, int dtype) 
 
 }  // namespace hbq
 
+// ---------------------------------------------------------------------------
+// scores of causal attention: s = R(R(s * scale) + bias) with bias 0 on and below
+// the diagonal and -inf above it, the two elementwise ops of src/module.py:96-112
+// (attn_weight = q @ k^T * scale_factor; attn_weight += attn_bias) in one pass.
+// torch computes both in fp32 on the T values (the scalar as fp32) and rounds
+// each result to T; so does this.  [mats, T, T], in place, 8 elements a thread.
+// ---------------------------------------------------------------------------
+template <class T>
+__global__ __launch_bounds__(kThreads) void scale_causal_mask_kernel(typename T::storage* __restrict__ s, int64_t mats,
+                                                                     int64_t Tn, float scale) {
+    const int64_t per_row = Tn / 8;
+    const int64_t total = mats * Tn * per_row;
+    const int64_t u = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (u >= total) return;
+    const int64_t row = u / per_row;
+    const int64_t c0 = (u - row * per_row) * 8;
+    const int64_t i = row % Tn;
+    u32x4 v = *reinterpret_cast<const u32x4*>(s + row * Tn + c0);
+    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint16_t b = (uint16_t)(w[e / 2] >> (16 * (e % 2)));
+        const float scaled = T::round(T::load(b) * scale);
+        const float out = T::round(scaled + (c0 + e > i ? -__builtin_inff() : 0.0f));
+        // torch's float -> bf16 conversion returns the canonical 0x7FC0 for every NaN
+        // (inf - inf gives a negative NaN here); its float -> fp16 conversion keeps the sign
+        const uint32_t o = (T::dt == kBF16 && out != out) ? 0x7FC0u : (uint32_t)T::store(out);
+        w[e / 2] = (e % 2) ? ((w[e / 2] & 0xffffu) | (o << 16)) : ((w[e / 2] & 0xffff0000u) | o);
+    }
+    *reinterpret_cast<u32x4*>(s + row * Tn + c0) = (u32x4){w[0], w[1], w[2], w[3]};
+}
+
 extern "C" {
 
 // Test hook: 1 routes every HBQ and MXFP / NVFP call to the generic kernels (so both can be checked).
@@ -478,6 +510,25 @@ int hbq_elem_quant(const void* x, void* y, void* codes, int64_t n, int dtype, in
 #undef ELEM_M
 #undef ELEM_CASE
     return hbq_check_launch("hbq_elem_quant");
+}
+
+int hbq_scale_causal_mask(void* s, int64_t mats, int64_t t, double scale, int dtype, void* stream) {
+    hbq_clear_error();
+    if (dtype != kF16 && dtype != kBF16) return hbq_fail(HBQ_ERR_UNSUPPORTED, "scores must be fp16 or bf16");
+    if (mats < 0 || t < 0) return hbq_fail(HBQ_ERR_INVALID, "negative size");
+    if (t % 8) return hbq_fail(HBQ_ERR_UNSUPPORTED, "the sequence length must be a multiple of 8");
+    if (mats == 0 || t == 0) return 0;
+    if (s == nullptr || (uintptr_t)s % 16) return hbq_fail(HBQ_ERR_INVALID, "scores must be 16-byte aligned");
+    const int64_t total = mats * t * (t / 8);
+    const int64_t grid = (total + kThreads - 1) / kThreads;
+    if (grid > 0x7fffffff) return hbq_fail(HBQ_ERR_INVALID, "tensor too large");
+    if (dtype == kF16)
+        hipLaunchKernelGGL(scale_causal_mask_kernel<F16>, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream,
+                           (uint16_t*)s, mats, t, (float)scale);
+    else
+        hipLaunchKernelGGL(scale_causal_mask_kernel<BF16>, dim3((unsigned)grid), dim3(kThreads), 0,
+                           (hipStream_t)stream, (uint16_t*)s, mats, t, (float)scale);
+    return hbq_check_launch("hbq_scale_causal_mask");
 }
 
 int hbq_flag_nonfinite(const void* x, int64_t rows, int64_t cols, int64_t ld, int dtype, int* flag, void* stream) {

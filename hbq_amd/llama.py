@@ -17,6 +17,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn as nn
 
+from . import _lib
 from .module import _QBaseLinear, deferred_finite_checks, forward_quantized_stacked, same_quantizer
 
 
@@ -60,6 +61,15 @@ def rotary(cfg, T, device):
     return emb.cos(), emb.sin()
 
 
+def scale_causal_mask_(s, scale):
+    """In place on [..., T, T] scores: s = R(R(s * scale) + bias), bias -inf above the diagonal
+    (src/module.py:96-112), one HIP pass with the bits of torch's two elementwise ops."""
+    T = s.shape[-1]
+    _lib.check(_lib.lib().hbq_scale_causal_mask(_lib.ptr(s), s.numel() // (T * T), T, float(scale),
+                                                _lib.DTYPE_CODE[s.dtype], _lib.stream_of(s)))
+    return s
+
+
 def _rotate_half(x):
     h = x.shape[-1] // 2
     return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
@@ -97,9 +107,13 @@ class QLlamaAttention(nn.Module):
         softmax (src/module.py:93-117)."""
         T = q.shape[-2]
         scale = 1.0 / math.sqrt(q.shape[-1])
-        s = torch.matmul(q, k.transpose(-2, -1).contiguous()) * scale
-        mask = torch.full((T, T), float("-inf"), device=q.device, dtype=s.dtype).triu(1)
-        s = s + mask
+        s = torch.matmul(q, k.transpose(-2, -1).contiguous())
+        if s.is_cuda and s.dtype in (torch.float16, torch.bfloat16) and T % 8 == 0 and s.is_contiguous() \
+                and s.shape[-1] == T:
+            scale_causal_mask_(s, scale)            # * scale, then + the causal bias, in one HIP pass
+        else:
+            s = s * scale
+            s = s + torch.full((T, T), float("-inf"), device=q.device, dtype=s.dtype).triu(1)
         p = torch.softmax(s, dim=-1)
         if self.quant_attn_wgt:
             p = self.attn_wgt_quantizer.q(p)

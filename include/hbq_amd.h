@@ -199,6 +199,14 @@ int hbq_gemm_group_partials(const void *A, const void *B, void *P, int64_t M, in
  * store 1, so one flag may collect several calls. */
 int hbq_flag_nonfinite(const void *x, int64_t rows, int64_t cols, int64_t ld, int dtype, int *flag, void *stream);
 
+/* Causal attention scores, in place: s = R(R(s * scale) + bias), bias 0 on and below
+ * the diagonal and -inf above, for mats [t, t] matrices of fp16 / bf16 (t % 8 == 0,
+ * s 16-byte aligned).  The two elementwise steps of the reference's manual attention
+ * (src/module.py:96-112: attn_weight = q @ k^T * scale_factor; attn_weight +=
+ * attn_bias) fused into one pass with the same bits (torch computes each in fp32 and
+ * rounds to the dtype; the scalar is converted to fp32). */
+int hbq_scale_causal_mask(void *s, int64_t mats, int64_t t, double scale, int dtype, void *stream);
+
 /* No reference counterpart: dst[cols, rows] = src[rows, cols]^T for 16-bit
  * elements.  The blockquant_ext front end uses it to hand a B[K,N] operand to
  * the W[N,K] kernels. */

@@ -201,3 +201,22 @@ def test_stacked_qkv_bit_identical(gpu, ops):
         sep2 = m(ids)
     assert torch.equal(sep2.view(torch.int16), st2.view(torch.int16))
     assert not torch.equal(st.view(torch.int16), st2.view(torch.int16))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_scale_causal_mask_matches_torch(gpu, dt):
+    """The fused scale + causal bias pass equals torch's `s * scale` then `s + bias`
+    (src/module.py:96-112) bit for bit, with -0, infinities and large values in the scores."""
+    from hbq_amd.llama import scale_causal_mask_
+    g = torch.Generator(device=gpu).manual_seed(12)
+    for T in (8, 64, 136):
+        s = (torch.randn(3, T, T, device=gpu, generator=g) * 40).to(dt)
+        s[0, 0, :4] = torch.tensor([-0.0, float("inf"), -float("inf"), 3e4], dtype=dt)
+        s[1, 5, 2] = -0.0
+        s[2, T - 1, T - 1] = torch.finfo(dt).max
+        scale = 1.0 / (128 ** 0.5)
+        ref = s * scale
+        ref = ref + torch.full((T, T), float("-inf"), device=gpu, dtype=dt).triu(1)
+        got = scale_causal_mask_(s.clone(), scale)
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), T
