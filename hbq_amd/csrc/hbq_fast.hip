@@ -299,8 +299,12 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
                             const h2_t e = xp[i / 2] - (h2_t){d0, d1};
                             h2_t q = e * e;
                             asm("" : "+v"(q));
-                            acc = i == sb * SUBN ? (float)q.x : acc + (float)q.x;
-                            acc += (float)q.y;
+                            // acc + (float)q.x, acc + (float)q.y, each one v_fma_mix_f32
+                            // (q * 1.0 + acc: the product is exact, so one fp32 rounding of
+                            // the sum, as v_add_f32 after a conversion)
+                            if (i == sb * SUBN) acc = (float)q.x;
+                            else asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel_hi:[1,0,0]" : "+v"(acc) : "v"(q));
+                            asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(acc) : "v"(q));
                         } else {
                             float e0, e1, q0, q1;
                             round2<T>(xa[i] - (float)d0, xa[i + 1] - (float)d1, e0, e1);
