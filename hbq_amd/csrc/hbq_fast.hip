@@ -235,6 +235,36 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
             l1[s] = sc != sc ? sc : e5m3_scale<T>(sc, p.use_ceil);
         }
 
+        // every block of this wave all zero (the masked half of causal attention weights):
+        // the reference's result is +0 everywhere, level 0, the first L2 candidate and
+        // scheme, and the L1 scale of a zero maximum computed above
+        if (!__builtin_amdgcn_ballot_w64(m2 != 0u)) {
+            if (valid) {
+                float zero[kV];
+#pragma unroll
+                for (int i = 0; i < kV; ++i) zero[i] = 0.f;
+                store16<T>(y + off, zero);
+                if (codes) {
+                    if constexpr (M == 1) *reinterpret_cast<uint2*>(codes + off / 2) = make_uint2(0u, 0u);
+                    else *reinterpret_cast<uint4*>(codes + off) = make_uint4(0u, 0u, 0u, 0u);
+                }
+                if (li == 0) {
+                    if (l1_out) l1_out[gb] = T::store(l1[0]);
+                    if (sch_out) sch_out[gb] = 0;
+                }
+                if (l2i_out) {
+                    constexpr int nsub_blk = block / L2B;
+                    if (L2B <= kV) {
+#pragma unroll
+                        for (int sb = 0; sb < NSUBL; ++sb) l2i_out[gb * nsub_blk + (li * kV) / L2B + sb] = 0;
+                    } else if ((li % LPS) == 0) {
+                        l2i_out[gb * nsub_blk + (li * kV) / L2B] = 0;
+                    }
+                }
+            }
+            continue;
+        }
+
         // magnitudes R_T(R_T(level * l2_j) * l1_s) of this block
 #pragma unroll
         for (int s = 0; s < S; ++s)

@@ -287,3 +287,30 @@ def test_mxfp_table_kernel_equals_generic(gpu, name):
     assert mismatches(to_bits(fast.y), to_bits(gen.y), "f16") == 0
     assert torch.equal(fast.codes, gen.codes)
     assert mismatches(to_bits(fast.scales), to_bits(gen.scales), "f16") == 0
+
+
+@pytest.mark.parametrize("name", ["hbq_a_act", "hbq_a_wgt", "hbq_kv4"])
+def test_hbq_causal_zero_blocks(gpu, oracle, name):
+    """Attention-weight-like input (row i zero past column i): waves whose eight blocks are all
+    zero take the table kernel's zero path; everything equals the oracle and the generic kernel."""
+    from hbq_amd import _lib
+    print(f"hbq causal zeros {name}", flush=True)
+    T = 2048
+    g = torch.Generator().manual_seed(23)
+    x = torch.softmax(torch.randn(64, T, generator=g) * 3, dim=-1)
+    rows = torch.arange(64)[:, None] * 32 + 7
+    x = torch.where(torch.arange(T)[None, :] > rows, torch.zeros(()), x).half()
+    q = _hbq(HBQCFG[name], keep_l2_scale=True)
+    y = q.q(x.to(gpu))
+    ref = oracle.hbq_qdq(to_bits(x), "f16", block_size=128, **HBQCFG[name])
+    assert mismatches(to_bits(y), ref["y"], "f16") == 0
+    assert mismatches(to_bits(q.shared_scale), ref["l1"], "f16") == 0
+    assert np.array_equal(q.l2_scale.cpu().numpy(), ref["l2idx"].astype(np.int64))
+    assert np.array_equal(q.blk_l2_scheme.cpu().numpy(), ref["scheme"].astype(np.int64))
+    fast = q.quantize(x.to(gpu))
+    old = _lib.lib().hbq_set_generic_only(1)
+    try:
+        gen = q.quantize(x.to(gpu))
+    finally:
+        _lib.lib().hbq_set_generic_only(old)
+    assert torch.equal(fast.codes, gen.codes)
