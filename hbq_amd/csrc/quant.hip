@@ -365,6 +365,53 @@ __global__ __launch_bounds__(kThreads) void scale_causal_mask_kernel(typename T:
     *reinterpret_cast<u32x4*>(s + row * Tn + c0) = (u32x4){w[0], w[1], w[2], w[3]};
 }
 
+// ---------------------------------------------------------------------------
+// rotary embedding of q or k: y = R(R(x * cos) + R(rotate_half(x) * sin)),
+// rotate_half(x) = cat(-x[d/2:], x[:d/2]), the three elementwise steps of the
+// Llama attention in one pass, read from the projection's strided [b, t, h, d]
+// view and written contiguous as [b, h, t, d].  Each step is torch's: fp32 on
+// the T values, rounded to T (bf16 NaNs become torch's canonical 0x7FC0).
+// cos / sin: [t, d] in T.  8 elements a thread.
+// ---------------------------------------------------------------------------
+template <class T>
+__global__ __launch_bounds__(kThreads) void rope_kernel(const typename T::storage* __restrict__ x,
+                                                        typename T::storage* __restrict__ y,
+                                                        const typename T::storage* __restrict__ cs,
+                                                        const typename T::storage* __restrict__ sn, int64_t B,
+                                                        int64_t H, int64_t Tn, int64_t D, int64_t sb, int64_t st,
+                                                        int64_t sh) {
+    const int64_t per_row = D / 8;
+    const int64_t u = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (u >= B * H * Tn * per_row) return;
+    const int64_t r = u / per_row, i0 = (u - r * per_row) * 8;
+    const int64_t t = r % Tn, r2 = r / Tn, h = r2 % H, bb = r2 / H;
+    const int64_t half = D / 2;
+    const bool lower = i0 < half;
+    const typename T::storage* xr = x + bb * sb + t * st + h * sh;
+    auto load8 = [](const typename T::storage* p, float* v) __attribute__((always_inline)) {
+        const u32x4 q = *reinterpret_cast<const u32x4*>(p);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = T::load((typename T::storage)(w[e / 2] >> (16 * (e % 2))));
+    };
+    float xv[8], xp[8], c[8], s8[8];
+    load8(xr + i0, xv);
+    load8(xr + (lower ? i0 + half : i0 - half), xp);
+    load8(cs + t * D + i0, c);
+    load8(sn + t * D + i0, s8);
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float a = T::round(xv[e] * c[e]);
+        const float rot = lower ? -xp[e] : xp[e];
+        const float b = T::round(rot * s8[e]);
+        const float out = T::round(a + b);
+        const uint32_t o = (T::dt == kBF16 && out != out) ? 0x7FC0u : (uint32_t)T::store(out);
+        w[e / 2] |= o << (16 * (e % 2));
+    }
+    *reinterpret_cast<u32x4*>(y + ((bb * H + h) * Tn + t) * D + i0) = (u32x4){w[0], w[1], w[2], w[3]};
+}
+
 extern "C" {
 
 // Test hook: 1 routes every HBQ and MXFP / NVFP call to the generic kernels (so both can be checked).
@@ -529,6 +576,31 @@ int hbq_scale_causal_mask(void* s, int64_t mats, int64_t t, double scale, int dt
         hipLaunchKernelGGL(scale_causal_mask_kernel<BF16>, dim3((unsigned)grid), dim3(kThreads), 0,
                            (hipStream_t)stream, (uint16_t*)s, mats, t, (float)scale);
     return hbq_check_launch("hbq_scale_causal_mask");
+}
+
+int hbq_rope(const void* x, void* y, const void* cos, const void* sin, int64_t b, int64_t h, int64_t t, int64_t d,
+             int64_t stride_b, int64_t stride_t, int64_t stride_h, int dtype, void* stream) {
+    hbq_clear_error();
+    if (dtype != kF16 && dtype != kBF16) return hbq_fail(HBQ_ERR_UNSUPPORTED, "rope takes fp16 or bf16");
+    if (b < 0 || h < 0 || t < 0 || d < 0) return hbq_fail(HBQ_ERR_INVALID, "negative size");
+    if (d % 16) return hbq_fail(HBQ_ERR_UNSUPPORTED, "rope needs head_dim %% 16 == 0");
+    if (b == 0 || h == 0 || t == 0 || d == 0) return 0;
+    if (!x || !y || !cos || !sin) return hbq_fail(HBQ_ERR_INVALID, "null pointer");
+    if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)cos | (uintptr_t)sin) % 16 || stride_b % 8 || stride_t % 8 ||
+        stride_h % 8)
+        return hbq_fail(HBQ_ERR_INVALID, "rope needs 16-byte aligned rows");
+    const int64_t total = b * h * t * (d / 8);
+    const int64_t grid = (total + kThreads - 1) / kThreads;
+    if (grid > 0x7fffffff) return hbq_fail(HBQ_ERR_INVALID, "tensor too large");
+    if (dtype == kF16)
+        hipLaunchKernelGGL(rope_kernel<F16>, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream,
+                           (const uint16_t*)x, (uint16_t*)y, (const uint16_t*)cos, (const uint16_t*)sin, b, h, t, d,
+                           stride_b, stride_t, stride_h);
+    else
+        hipLaunchKernelGGL(rope_kernel<BF16>, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream,
+                           (const uint16_t*)x, (uint16_t*)y, (const uint16_t*)cos, (const uint16_t*)sin, b, h, t, d,
+                           stride_b, stride_t, stride_h);
+    return hbq_check_launch("hbq_rope");
 }
 
 int hbq_flag_nonfinite(const void* x, int64_t rows, int64_t cols, int64_t ld, int dtype, int* flag, void* stream) {

@@ -70,6 +70,23 @@ def scale_causal_mask_(s, scale):
     return s
 
 
+def _rope_ok(x):
+    return (x.is_cuda and x.dtype in (torch.float16, torch.bfloat16) and x.shape[-1] % 16 == 0
+            and x.stride(-1) == 1 and all(st % 8 == 0 for st in x.stride()[:-1]) and x.data_ptr() % 16 == 0)
+
+
+def rope(x, cos, sin):
+    """x [b, t, h, d] (any strides with unit stride on d) -> contiguous [b, h, t, d] of
+    x * cos + rotate_half(x) * sin, one HIP pass with the bits of torch's elementwise ops;
+    cos, sin [t, d] contiguous in x's dtype."""
+    b, T, h, d = x.shape
+    y = torch.empty((b, h, T, d), dtype=x.dtype, device=x.device)
+    _lib.check(_lib.lib().hbq_rope(_lib.ptr(x), _lib.ptr(y), _lib.ptr(cos), _lib.ptr(sin), b, h, T, d,
+                                   x.stride(0), x.stride(1), x.stride(2), _lib.DTYPE_CODE[x.dtype],
+                                   _lib.stream_of(x)))
+    return y
+
+
 def _rotate_half(x):
     h = x.shape[-1] // 2
     return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
@@ -131,10 +148,15 @@ class QLlamaAttention(nn.Module):
                 q, k, v = qp.forward_quantized(xq), kp.forward_quantized(xq), vp.forward_quantized(xq)
         else:
             q, k, v = qp(x), kp(x), vp(x)
-        q = q.view(b, T, self.num_heads, self.head_dim).transpose(1, 2)
-        k = k.view(b, T, self.num_key_value_heads, self.head_dim).transpose(1, 2)
+        q = q.view(b, T, self.num_heads, self.head_dim)
+        k = k.view(b, T, self.num_key_value_heads, self.head_dim)
         v = v.view(b, T, self.num_key_value_heads, self.head_dim).transpose(1, 2)
-        q, k = apply_rope(q, k, cos, sin)
+        if _rope_ok(q) and _rope_ok(k):
+            # one HIP pass each, written contiguous [b, h, t, d] (src/module.py:153-158)
+            c16, s16 = cos.to(q.dtype).contiguous(), sin.to(q.dtype).contiguous()
+            q, k = rope(q, c16, s16), rope(k, c16, s16)
+        else:
+            q, k = apply_rope(q.transpose(1, 2), k.transpose(1, 2), cos, sin)
         if self.quant_post_rope_q:
             q = self.q_proj.aq.q(q)
         if self.quant_k_cache:

@@ -207,6 +207,16 @@ int hbq_flag_nonfinite(const void *x, int64_t rows, int64_t cols, int64_t ld, in
  * rounds to the dtype; the scalar is converted to fp32). */
 int hbq_scale_causal_mask(void *s, int64_t mats, int64_t t, double scale, int dtype, void *stream);
 
+/* Rotary embedding of the decoder's q or k (no counterpart kernel: the elementwise
+ * q * cos + rotate_half(q) * sin of the Llama attention the quantization points sit
+ * in, apply_rotary_pos_emb at src/module.py:153-158): y[b, h, t, :] = R(R(x * cos[t]) + R(rotate_half(x) * sin[t]))
+ * with rotate_half(x) = cat(-x[d/2:], x[:d/2]), each step as torch computes it.  x is
+ * read as [b, t, h, d] with element strides (stride_b, stride_t, stride_h, 1), y is
+ * written contiguous [b, h, t, d]; cos, sin [t, d] in the same dtype (fp16 / bf16);
+ * d % 16 == 0, rows 16-byte aligned. */
+int hbq_rope(const void *x, void *y, const void *cos, const void *sin, int64_t b, int64_t h, int64_t t, int64_t d,
+             int64_t stride_b, int64_t stride_t, int64_t stride_h, int dtype, void *stream);
+
 /* No reference counterpart: dst[cols, rows] = src[rows, cols]^T for 16-bit
  * elements.  The blockquant_ext front end uses it to hand a B[K,N] operand to
  * the W[N,K] kernels. */

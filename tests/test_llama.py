@@ -220,3 +220,23 @@ def test_scale_causal_mask_matches_torch(gpu, dt):
         ref = ref + torch.full((T, T), float("-inf"), device=gpu, dtype=dt).triu(1)
         got = scale_causal_mask_(s.clone(), scale)
         assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), T
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_rope_matches_torch(gpu, dt):
+    """The fused rotary pass equals torch's q * cos + rotate_half(q) * sin bit for bit, read from
+    a strided [b, t, h, d] view (a column slice of the stacked q/k/v output) and written
+    contiguous [b, h, t, d]."""
+    from hbq_amd.llama import LlamaConfig, apply_rope, rope, rotary
+    g = torch.Generator(device=gpu).manual_seed(13)
+    b, T, H, d = 2, 96, 4, 64
+    full = (torch.randn(b, T, 3 * H * d, device=gpu, generator=g) * 8).to(dt)
+    full[0, 0, :8] = torch.tensor([-0.0, float("inf"), -float("inf"), float("nan"), 6e4, -6e4, 1e-7, -1e-7],
+                                  dtype=torch.float32).to(dt)
+    x = full[..., H * d: 2 * H * d].view(b, T, H, d)          # strided like the k slice
+    cos, sin = rotary(LlamaConfig(hidden_size=H * d, num_attention_heads=H, num_key_value_heads=H), T, gpu)
+    ref, _ = apply_rope(x.transpose(1, 2), x.transpose(1, 2), cos, sin)
+    got = rope(x, cos.to(dt).contiguous(), sin.to(dt).contiguous())
+    assert got.is_contiguous() and got.shape == ref.shape
+    assert torch.equal(got.view(torch.int16), ref.contiguous().view(torch.int16))
