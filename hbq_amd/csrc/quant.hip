@@ -412,6 +412,58 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(const typename T::storag
     *reinterpret_cast<u32x4*>(y + ((bb * H + h) * Tn + t) * D + i0) = (u32x4){w[0], w[1], w[2], w[3]};
 }
 
+// ---------------------------------------------------------------------------
+// causal attention probabilities from raw scores, in one pass:
+//   e = R(R(s * scale) + bias)    (bias -inf above the diagonal; src/module.py:96-112)
+//   p = softmax(e) along the row  (src/module.py:113, torch.softmax in fp32, rounded to T)
+// The softmax follows torch's persistent warp softmax step for step, so the bits are
+// torch's: one wave (64 lanes) per row, lane l holding columns l + 64 it; the row max
+// by a sequential "a > b ? a : b" over its elements, then a butterfly over the lanes
+// with "a < b ? b : a"; sum += exp(e - max) in column order, butterfly-added; p =
+// exp(e - max) / sum (a NaN row for sum == 0), rounded to T (bf16 NaNs 0x7FC0).
+// [mats, t, t] with t = 64 ITER, in place allowed (a row is read before it is written).
+// ---------------------------------------------------------------------------
+template <class T, int ITER>
+__global__ __launch_bounds__(kThreads) void causal_softmax_kernel(const typename T::storage* __restrict__ s,
+                                                                  typename T::storage* p, int64_t rows,
+                                                                  float scale) {
+    constexpr int Tn = 64 * ITER;
+    const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    if (row >= rows) return;   // whole waves
+    const int lane = threadIdx.x & 63;
+    const int64_t i = row % Tn;
+    const typename T::storage* src = s + row * Tn;
+    float el[ITER];
+#pragma unroll
+    for (int it = 0; it < ITER; ++it) {
+        const int c = lane + 64 * it;
+        const float scaled = T::round(T::load(src[c]) * scale);
+        el[it] = T::round(scaled + (c > i ? -__builtin_inff() : 0.0f));
+    }
+    float mx = el[0];
+#pragma unroll
+    for (int it = 0; it < ITER; ++it) mx = mx > el[it] ? mx : el[it];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float b = __shfl_xor(mx, off, 64);
+        mx = mx < b ? b : mx;
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int it = 0; it < ITER; ++it) {
+        el[it] = expf(el[it] - mx);
+        sum += el[it];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum = sum + __shfl_xor(sum, off, 64);
+    typename T::storage* dst = p + row * Tn;
+#pragma unroll
+    for (int it = 0; it < ITER; ++it) {
+        const float v = sum == 0.f ? __builtin_nanf("") : el[it] / sum;
+        dst[lane + 64 * it] = (T::dt == kBF16 && v != v) ? (typename T::storage)0x7FC0u : T::store(v);
+    }
+}
+
 extern "C" {
 
 // Test hook: 1 routes every HBQ and MXFP / NVFP call to the generic kernels (so both can be checked).
@@ -576,6 +628,37 @@ int hbq_scale_causal_mask(void* s, int64_t mats, int64_t t, double scale, int dt
         hipLaunchKernelGGL(scale_causal_mask_kernel<BF16>, dim3((unsigned)grid), dim3(kThreads), 0,
                            (hipStream_t)stream, (uint16_t*)s, mats, t, (float)scale);
     return hbq_check_launch("hbq_scale_causal_mask");
+}
+
+int hbq_causal_softmax(const void* s, void* p, int64_t mats, int64_t t, double scale, int dtype, void* stream) {
+    hbq_clear_error();
+    if (dtype != kF16 && dtype != kBF16) return hbq_fail(HBQ_ERR_UNSUPPORTED, "scores must be fp16 or bf16");
+    if (mats < 0) return hbq_fail(HBQ_ERR_INVALID, "negative size");
+    if (t != 64 && t != 128 && t != 256 && t != 512 && t != 1024 && t != 2048)
+        return hbq_fail(HBQ_ERR_UNSUPPORTED, "the fused causal softmax takes t = 64, 128, ..., 2048");
+    if (mats == 0) return 0;
+    if (!s || !p) return hbq_fail(HBQ_ERR_INVALID, "null pointer");
+    const int64_t rows = mats * t;
+    const int64_t grid = (rows + (kThreads / 64) - 1) / (kThreads / 64);
+    if (grid > 0x7fffffff) return hbq_fail(HBQ_ERR_INVALID, "tensor too large");
+    hipStream_t st = (hipStream_t)stream;
+    const float sc = (float)scale;
+#define CSM(TT, IT)                                                                                        \
+    hipLaunchKernelGGL((causal_softmax_kernel<TT, IT>), dim3((unsigned)grid), dim3(kThreads), 0, st,       \
+                       (const uint16_t*)s, (uint16_t*)p, rows, sc)
+#define CSM_T(TT)                                                                                          \
+    switch (t) {                                                                                           \
+        case 64: CSM(TT, 1); break;                                                                        \
+        case 128: CSM(TT, 2); break;                                                                       \
+        case 256: CSM(TT, 4); break;                                                                       \
+        case 512: CSM(TT, 8); break;                                                                       \
+        case 1024: CSM(TT, 16); break;                                                                     \
+        default: CSM(TT, 32); break;                                                                       \
+    }
+    if (dtype == kF16) { CSM_T(F16) } else { CSM_T(BF16) }
+#undef CSM_T
+#undef CSM
+    return hbq_check_launch("hbq_causal_softmax");
 }
 
 int hbq_rope(const void* x, void* y, const void* cos, const void* sin, int64_t b, int64_t h, int64_t t, int64_t d,

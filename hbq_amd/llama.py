@@ -70,6 +70,16 @@ def scale_causal_mask_(s, scale):
     return s
 
 
+def causal_softmax_(s, scale):
+    """In place on [..., T, T] raw scores: softmax(R(R(s * scale) + bias)) along the rows, bias -inf
+    above the diagonal (src/module.py:96-113), one HIP pass with the bits of torch's ops
+    (T a power of two from 64 to 2048)."""
+    T = s.shape[-1]
+    _lib.check(_lib.lib().hbq_causal_softmax(_lib.ptr(s), _lib.ptr(s), s.numel() // (T * T), T, float(scale),
+                                             _lib.DTYPE_CODE[s.dtype], _lib.stream_of(s)))
+    return s
+
+
 def _rope_ok(x):
     return (x.is_cuda and x.dtype in (torch.float16, torch.bfloat16) and x.shape[-1] % 16 == 0
             and x.stride(-1) == 1 and all(st % 8 == 0 for st in x.stride()[:-1]) and x.data_ptr() % 16 == 0)
@@ -125,13 +135,16 @@ class QLlamaAttention(nn.Module):
         T = q.shape[-2]
         scale = 1.0 / math.sqrt(q.shape[-1])
         s = torch.matmul(q, k.transpose(-2, -1).contiguous())
-        if s.is_cuda and s.dtype in (torch.float16, torch.bfloat16) and T % 8 == 0 and s.is_contiguous() \
-                and s.shape[-1] == T:
-            scale_causal_mask_(s, scale)            # * scale, then + the causal bias, in one HIP pass
+        fused = s.is_cuda and s.dtype in (torch.float16, torch.bfloat16) and s.is_contiguous() and s.shape[-1] == T
+        if fused and T in (64, 128, 256, 512, 1024, 2048):
+            p = causal_softmax_(s, scale)           # * scale, + the causal bias and softmax: one HIP pass
         else:
-            s = s * scale
-            s = s + torch.full((T, T), float("-inf"), device=q.device, dtype=s.dtype).triu(1)
-        p = torch.softmax(s, dim=-1)
+            if fused and T % 8 == 0:
+                scale_causal_mask_(s, scale)        # * scale, then + the causal bias, in one HIP pass
+            else:
+                s = s * scale
+                s = s + torch.full((T, T), float("-inf"), device=q.device, dtype=s.dtype).triu(1)
+            p = torch.softmax(s, dim=-1)
         if self.quant_attn_wgt:
             p = self.attn_wgt_quantizer.q(p)
         return torch.matmul(p, v), p

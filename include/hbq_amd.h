@@ -207,6 +207,14 @@ int hbq_flag_nonfinite(const void *x, int64_t rows, int64_t cols, int64_t ld, in
  * rounds to the dtype; the scalar is converted to fp32). */
 int hbq_scale_causal_mask(void *s, int64_t mats, int64_t t, double scale, int dtype, void *stream);
 
+/* Causal attention probabilities from raw scores, in place allowed (no counterpart
+ * kernel): the scaling and causal bias of hbq_scale_causal_mask followed by
+ * torch.softmax along the rows (src/module.py:96-113), one pass over the scores.  The
+ * softmax repeats torch's persistent warp softmax step for step (row max and sum per
+ * 64-lane wave in its element order and butterfly order, exp, division), so p has
+ * torch's bits.  [mats, t, t] fp16 / bf16 with t a power of two from 64 to 2048. */
+int hbq_causal_softmax(const void *s, void *p, int64_t mats, int64_t t, double scale, int dtype, void *stream);
+
 /* Rotary embedding of the decoder's q or k (no counterpart kernel: the elementwise
  * q * cos + rotate_half(q) * sin of the Llama attention the quantization points sit
  * in, apply_rotary_pos_emb at src/module.py:153-158): y[b, h, t, :] = R(R(x * cos[t]) + R(rotate_half(x) * sin[t]))

@@ -240,3 +240,27 @@ def test_rope_matches_torch(gpu, dt):
     got = rope(x, cos.to(dt).contiguous(), sin.to(dt).contiguous())
     assert got.is_contiguous() and got.shape == ref.shape
     assert torch.equal(got.view(torch.int16), ref.contiguous().view(torch.int16))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_causal_softmax_matches_torch(gpu, dt):
+    """The fused scale + causal bias + softmax pass equals torch's `s * scale`, `s + bias` and
+    `torch.softmax` bit for bit, rows with infinities and NaN included."""
+    from hbq_amd.llama import causal_softmax_
+    g = torch.Generator(device=gpu).manual_seed(14)
+    scale = 1.0 / (128 ** 0.5)
+    for T in (64, 128, 256, 2048):
+        mats = 3 if T < 2048 else 2
+        s = (torch.randn(mats, T, T, device=gpu, generator=g) * 30).to(dt)
+        s[0, 5, 2] = float("inf")            # unmasked +inf: NaN row in torch
+        s[0, 6, 9] = float("inf")            # masked +inf: inf - inf = NaN as well
+        s[0, 7, 3] = -float("inf")
+        s[1, 8, 1] = float("nan")
+        s[1, T - 1, :] = -6e4 if dt == torch.float16 else -3e38
+        ref = s * scale
+        ref = ref + torch.full((T, T), float("-inf"), device=gpu, dtype=dt).triu(1)
+        ref = torch.softmax(ref, dim=-1)
+        got = causal_softmax_(s.clone(), scale)
+        same = got.view(torch.int16) == ref.view(torch.int16)
+        assert bool(same.all()), (T, int((~same).sum()))
