@@ -34,6 +34,9 @@ SIGNATURES = {
     "hbq_flag_nonfinite": ([_P, _I64, _I64, _I64, _I, _P, _P], _I),
     "hbq_scale_causal_mask": ([_P, _I64, _I64, ctypes.c_double, _I, _P], _I),
     "hbq_causal_softmax": ([_P, _P, _I64, _I64, ctypes.c_double, _I, _P], _I),
+    "hbq_rms_prep": ([_P, _P, _P, _P, _I64, _I, _P], _I),
+    "hbq_rms_apply": ([_P, _P, _P, _P, _I64, _I64, _I, _P], _I),
+    "hbq_silu_mul": ([_P, _P, _P, _I64, _I, _P], _I),
     "hbq_rope": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P], _I),
     "hbq_hbq_packed_strides": ([_I64, _I, _I, _I, _I, _I, _P], _I),
     "hbq_hbq_pack": ([_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _I, _P], _I),

@@ -19,7 +19,7 @@ OUT_DIR = os.path.join(HERE, "_lib")
 LIB = os.path.join(OUT_DIR, "libhbq_amd.so")
 ARCH = os.environ.get("HBQ_OFFLOAD_ARCH", "gfx950")
 
-HIP_SOURCES = ["quant.hip", "hbq_fast.hip", "mx_fast.hip", "gemm.hip", "gemm_tile256.hip", "pack.hip", "gemm_packed.hip"]
+HIP_SOURCES = ["quant.hip", "hbq_fast.hip", "mx_fast.hip", "gemm.hip", "gemm_tile256.hip", "pack.hip", "gemm_packed.hip", "model_ops.hip"]
 CXX_SOURCES = ["capi.cpp"]
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", "-Wno-unused-function"]
 HIP_FLAGS = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]

@@ -51,6 +51,49 @@ class RMSNorm(nn.Module):
         h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + self.eps)
         return self.weight * h.to(dt)
 
+    def add_norm(self, x, res=None):
+        """(x + res, norm(x + res)), or (x, norm(x)) without res: the residual add and the
+        norm of the decoder with the bits of the torch ops above.  On the GPU two HIP passes
+        (the add with the fp32 squares; the product, conversion and weight) around torch's
+        own row mean of the squares and rsqrt, whose reduction order and rsqrt fix the bits."""
+        if _fused_norm_ok(x, res, self.weight):
+            s = torch.empty_like(x) if res is not None else x
+            sq = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+            st = _lib.stream_of(x)
+            _lib.check(_lib.lib().hbq_rms_prep(_lib.ptr(x), _lib.ptr(res), _lib.ptr(s) if res is not None else None,
+                                               _lib.ptr(sq), x.numel(), _lib.DTYPE_CODE[x.dtype], st))
+            rs = torch.rsqrt(sq.mean(-1, keepdim=True) + self.eps)
+            y = torch.empty_like(x)
+            _lib.check(_lib.lib().hbq_rms_apply(_lib.ptr(s), _lib.ptr(rs), _lib.ptr(self.weight), _lib.ptr(y),
+                                                x.numel() // x.shape[-1], x.shape[-1], _lib.DTYPE_CODE[x.dtype], st))
+            return s, y
+        if res is not None:
+            x = x + res
+        return x, self.forward(x)
+
+
+def _fused_ok(*ts):
+    t0 = ts[0]
+    return (t0.is_cuda and t0.dtype in (torch.float16, torch.bfloat16) and t0.numel() % 8 == 0
+            and all(t is None or (t.dtype == t0.dtype and t.device == t0.device and t.is_contiguous()
+                                  and t.data_ptr() % 16 == 0) for t in ts))
+
+
+def _fused_norm_ok(x, res, w):
+    return (_fused_ok(x, res, w) and x.shape[-1] % 8 == 0 and w.dim() == 1 and w.shape[0] == x.shape[-1]
+            and (res is None or res.shape == x.shape))
+
+
+def silu_mul(gate, up):
+    """silu(gate) * up with torch's bits (two rounded ops), one HIP pass; None when the
+    tensors do not fit the kernel."""
+    if not (_fused_ok(gate, up) and gate.shape == up.shape):
+        return None
+    y = torch.empty_like(gate)
+    _lib.check(_lib.lib().hbq_silu_mul(_lib.ptr(gate), _lib.ptr(up), _lib.ptr(y), gate.numel(),
+                                       _lib.DTYPE_CODE[gate.dtype], _lib.stream_of(gate)))
+    return y
+
 
 def rotary(cfg, T, device):
     """cos, sin [T, head_dim] (fp32) of the rotary embedding."""
@@ -131,10 +174,15 @@ class QLlamaAttention(nn.Module):
 
     def manual_sdpa(self, q, k, v):
         """Causal softmax(q k^T / sqrt(d)) v with the attention weights quantized after the
-        softmax (src/module.py:93-117)."""
-        T = q.shape[-2]
-        scale = 1.0 / math.sqrt(q.shape[-1])
-        s = torch.matmul(q, k.transpose(-2, -1).contiguous())
+        softmax (src/module.py:93-117).  q [b, H, T, d]; k, v [b, KVH, T, d] with the query
+        heads of one kv head consecutive (repeat_kv's order): each kv head's rep = H / KVH
+        query heads multiply it as one [rep * T, d] operand, which reads the same scores and
+        outputs as the repeated k and v without copying them."""
+        b, H, T, d = q.shape
+        kvh = k.shape[1]
+        scale = 1.0 / math.sqrt(d)
+        qg = q.reshape(b, kvh, (H // kvh) * T, d)
+        s = torch.matmul(qg, k.transpose(-2, -1).contiguous()).view(b, H, T, T)
         fused = s.is_cuda and s.dtype in (torch.float16, torch.bfloat16) and s.is_contiguous() and s.shape[-1] == T
         if fused and T in (64, 128, 256, 512, 1024, 2048):
             p = causal_softmax_(s, scale)           # * scale, + the causal bias and softmax: one HIP pass
@@ -147,7 +195,7 @@ class QLlamaAttention(nn.Module):
             p = torch.softmax(s, dim=-1)
         if self.quant_attn_wgt:
             p = self.attn_wgt_quantizer.q(p)
-        return torch.matmul(p, v), p
+        return torch.matmul(p.view(b, kvh, (H // kvh) * T, T), v).view(b, H, T, d), p
 
     def forward(self, x, cos, sin):
         b, T, _ = x.shape
@@ -177,9 +225,6 @@ class QLlamaAttention(nn.Module):
         if self.quant_v_cache:
             # V is quantized along the tokens: the following product is P @ V
             v = self.kv_quantizer.q(v.transpose(-1, -2).contiguous()).transpose(-1, -2).contiguous()
-        rep = self.num_heads // self.num_key_value_heads
-        k = k.repeat_interleave(rep, dim=1)
-        v = v.repeat_interleave(rep, dim=1)
         out, _ = self.manual_sdpa(q.contiguous(), k.contiguous(), v.contiguous())
         out = out.transpose(1, 2).contiguous().view(b, T, -1)
         return self.o_proj(out)
@@ -201,6 +246,10 @@ class QLlamaMLP(nn.Module):
             gate, up = self.gate_proj.forward_quantized(xq), self.up_proj.forward_quantized(xq)
         else:
             gate, up = self.gate_proj(x), self.up_proj(x)
+        if self.quantizer_after_act_fn is None:
+            y = silu_mul(gate, up)
+            if y is not None:
+                return self.down_proj(y)
         g = torch.nn.functional.silu(gate)
         if self.quantizer_after_act_fn is not None:
             g = self.quantizer_after_act_fn.q(g)
@@ -215,9 +264,12 @@ class DecoderLayer(nn.Module):
         self.post_attention_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
         self.mlp = QLlamaMLP(cfg)
 
-    def forward(self, x, cos, sin):
-        x = x + self.self_attn(self.input_layernorm(x), cos, sin)
-        return x + self.mlp(self.post_attention_layernorm(x))
+    def forward(self, x, cos, sin, res=None):
+        """(x, r) with x + r the layer's output, for input x + res: the residual add
+        that ends a layer is left to the next norm, which fuses it."""
+        x, h = self.input_layernorm.add_norm(x, res)
+        x, h = self.post_attention_layernorm.add_norm(x, self.self_attn(h, cos, sin))
+        return x, self.mlp(h)
 
 
 class LlamaForCausalLM(nn.Module):
@@ -244,6 +296,8 @@ class LlamaForCausalLM(nn.Module):
         with deferred_finite_checks():
             x = self.embed_tokens(ids)
             cos, sin = rotary(self.config, ids.shape[1], ids.device)
+            cos, sin = cos.to(x.dtype), sin.to(x.dtype)    # as every layer's apply_rotary_pos_emb casts them
+            res = None
             for layer in self.layers:
-                x = layer(x, cos, sin)
-            return self.lm_head(self.norm(x))
+                x, res = layer(x, cos, sin, res)
+            return self.lm_head(self.norm.add_norm(x, res)[1])

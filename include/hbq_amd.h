@@ -225,6 +225,29 @@ int hbq_causal_softmax(const void *s, void *p, int64_t mats, int64_t t, double s
 int hbq_rope(const void *x, void *y, const void *cos, const void *sin, int64_t b, int64_t h, int64_t t, int64_t d,
              int64_t stride_b, int64_t stride_t, int64_t stride_h, int dtype, void *stream);
 
+/* Decoder plumbing around the quantized linears (no reference kernels: the Hugging Face
+ * Llama modules that src/module.py patches, in torch ops).  Each reproduces torch's
+ * eager ops bit for bit: every op in fp32 on the fp16 / bf16 values, rounded to the
+ * dtype once per op; n and cols multiples of 8, tensors 16-byte aligned.
+ *
+ * RMSNorm, first half: sum = R(x + res) when res is non-null (the residual add
+ * before the norm; sum may alias x), and sq = s * s in fp32 of s = sum or x
+ * (h.float().pow(2)).  The row mean of sq is left to torch.mean, whose reduction
+ * order it keeps. */
+int hbq_rms_prep(const void *x, const void *res, void *sum, float *sq, int64_t n, int dtype, void *stream);
+
+/* RMSNorm, second half: y = R(w * R(R32(x * rs[row]))), the `h * rs`, `.to(dtype)`
+ * and `weight *` steps of LlamaRMSNorm with rs = torch.rsqrt(var + eps) [rows] fp32
+ * from torch (its rsqrt and this library's can differ in the last bit); w [cols] in
+ * the dtype. */
+int hbq_rms_apply(const void *x, const float *rs, const void *w, void *y, int64_t rows, int64_t cols, int dtype,
+                  void *stream);
+
+/* The gated MLP product y = R(R(silu(g)) * u), silu(g) = g / (1 + exp(-g)) in fp32
+ * (torch.nn.functional.silu(gate) * up of QLlamaMLP, src/module.py:547-569, without
+ * a quantizer after the activation). */
+int hbq_silu_mul(const void *g, const void *u, void *y, int64_t n, int dtype, void *stream);
+
 /* No reference counterpart: dst[cols, rows] = src[rows, cols]^T for 16-bit
  * elements.  The blockquant_ext front end uses it to hand a B[K,N] operand to
  * the W[N,K] kernels. */

@@ -264,3 +264,63 @@ def test_causal_softmax_matches_torch(gpu, dt):
         got = causal_softmax_(s.clone(), scale)
         same = got.view(torch.int16) == ref.view(torch.int16)
         assert bool(same.all()), (T, int((~same).sum()))
+
+
+def test_grouped_query_attention_equals_repeated_kv_cpu():
+    """The attention that multiplies each kv head by its query heads as one operand equals
+    the one on repeat_interleave'd k and v (repeat_kv), up to the fp32 summation order."""
+    torch.manual_seed(3)
+    a = LlamaForCausalLM(TINY).layers[0].self_attn
+    H, KVH, T, d = TINY.num_attention_heads, TINY.num_key_value_heads, 32, TINY.head_dim
+    q = torch.randn(2, H, T, d)
+    k = torch.randn(2, KVH, T, d)
+    v = torch.randn(2, KVH, T, d)
+    out, p = a.manual_sdpa(q, k, v)
+    kr, vr = k.repeat_interleave(H // KVH, dim=1), v.repeat_interleave(H // KVH, dim=1)
+    s = q @ kr.transpose(-2, -1) / d ** 0.5 + torch.full((T, T), float("-inf")).triu(1)
+    pr = torch.softmax(s, dim=-1)
+    assert p.shape == (2, H, T, T)
+    torch.testing.assert_close(p, pr, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(out, pr @ vr, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_add_rmsnorm_matches_torch(gpu, dt):
+    """The fused residual add + RMSNorm equals x + res and the torch RMSNorm bit for bit,
+    infinities and NaN included; without res, the norm alone."""
+    from hbq_amd.llama import RMSNorm
+    g = torch.Generator(device=gpu).manual_seed(21)
+    norm = RMSNorm(1024, 1e-5).to(gpu).to(dt)
+    with torch.no_grad():
+        norm.weight.copy_(torch.randn(1024, device=gpu, generator=g) * 0.5 + 1)
+    x = (torch.randn(64, 1024, device=gpu, generator=g) * 3).to(dt)
+    res = (torch.randn(64, 1024, device=gpu, generator=g) * 2).to(dt)
+    x[0, :] = x[0, :] * 1e-3                 # tiny rows
+    x[1, :] = 60000.0 if dt == torch.float16 else 1e30
+    res[2, 5] = float("inf")
+    res[3, 7] = float("nan")
+    with torch.no_grad():
+        s, y = norm.add_norm(x, res)
+        s_ref = x + res
+        y_ref = norm(s_ref)
+        y0, y0_ref = norm.add_norm(x)[1], norm(x)
+    for name, got, ref in (("sum", s, s_ref), ("norm", y, y_ref), ("norm alone", y0, y0_ref)):
+        same = got.view(torch.int16) == ref.view(torch.int16)
+        bad = (~same).nonzero()[:4].tolist()
+        assert bool(same.all()), (name, int((~same).sum()), [(i, float(got[i[0], i[1]]), float(ref[i[0], i[1]]))
+                                                            for i in bad])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_silu_mul_matches_torch(gpu, dt):
+    """silu(gate) * up in one HIP pass equals torch's two ops bit for bit, over every 16-bit
+    pattern of the gate."""
+    from hbq_amd.llama import silu_mul
+    gate = torch.arange(-32768, 32768, dtype=torch.int32, device=gpu).to(torch.int16).view(dt)
+    up = torch.randn(gate.shape, device=gpu, generator=torch.Generator(device=gpu).manual_seed(4)).to(dt) * 4
+    got = silu_mul(gate, up)
+    ref = torch.nn.functional.silu(gate) * up
+    same = got.view(torch.int16) == ref.view(torch.int16)
+    assert bool(same.all()), int((~same).sum())
