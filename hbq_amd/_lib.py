@@ -34,6 +34,7 @@ SIGNATURES = {
     "hbq_flag_nonfinite": ([_P, _I64, _I64, _I64, _I, _P, _P], _I),
     "hbq_scale_causal_mask": ([_P, _I64, _I64, ctypes.c_double, _I, _P], _I),
     "hbq_causal_softmax": ([_P, _P, _I64, _I64, ctypes.c_double, _I, _P], _I),
+    "hbq_hbq_qdq_causal": ([_P, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "hbq_rms_prep": ([_P, _P, _P, _P, _I64, _I, _P], _I),
     "hbq_rms_apply": ([_P, _P, _P, _P, _I64, _I64, _I, _P], _I),
     "hbq_silu_mul": ([_P, _P, _P, _I64, _I, _P], _I),
@@ -60,6 +61,10 @@ def lib():
                 fn.restype = res
         _lib = L
     return _lib
+
+
+# return codes of the C-ABI (include/hbq_amd.h)
+ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP = 1, 2, 3
 
 
 def check(rc, exc=RuntimeError):

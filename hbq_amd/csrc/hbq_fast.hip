@@ -150,8 +150,8 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
                                                             typename T::storage* __restrict__ l1_out,
                                                             uint8_t* __restrict__ l2i_out,
                                                             uint8_t* __restrict__ sch_out,
-                                                            uint8_t* __restrict__ codes, int64_t nb, int slot,
-                                                            FastParams p) {
+                                                            uint8_t* __restrict__ codes, int64_t nb, int64_t causal_t,
+                                                            int slot, FastParams p) {
     using DT = DTabT<T>;
     constexpr int lpb = 8;
     constexpr int bpw = 64 / lpb;
@@ -192,8 +192,30 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
     const int64_t ntiles = (nb + blocks_per_wg - 1) / blocks_per_wg;
     const float tiny = T::dt == kF16 ? 6.103515625e-05f : 1.17549435e-38f;
 
-    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-        const int64_t gb = tile * blocks_per_wg + (threadIdx.x / lpb);
+    // causal_t > 0: nb blocks of [mats, t, t] attention weights whose blocks above the
+    // diagonal are zero and stay as they are (y == x): each wave takes one column block of
+    // 8 consecutive rows among the blocks on or below the diagonal.  Rows 128k .. 128k+127
+    // of a matrix (band k, 16 groups of 8 rows) hold k + 1 such blocks.
+    const int64_t nbt = causal_t / block;
+    const int64_t per_mat = 8 * nbt * (nbt + 1);
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int64_t nwork = causal_t ? nb / (causal_t * nbt) * per_mat : ntiles;
+    const int64_t first = causal_t ? (int64_t)blockIdx.x * (kThreads / 64) + wave : (int64_t)blockIdx.x;
+    const int64_t stride = causal_t ? (int64_t)gridDim.x * (kThreads / 64) : (int64_t)gridDim.x;
+
+    for (int64_t tile = first; tile < nwork; tile += stride) {
+        int64_t gb;
+        if (causal_t) {
+            const int64_t m = tile / per_mat;
+            const int64_t r = tile - m * per_mat;
+            int64_t k = 0;
+            while (8 * (k + 1) * (k + 2) <= r) ++k;
+            const int64_t r2 = r - 8 * k * (k + 1);
+            const int64_t rg = r2 / (k + 1), cb = r2 - rg * (k + 1);
+            gb = (m * causal_t + 128 * k + 8 * rg + bw) * nbt + cb;
+        } else {
+            gb = tile * blocks_per_wg + (threadIdx.x / lpb);
+        }
         const bool valid = gb < nb;
         const int64_t off = (valid ? gb : 0) * (int64_t)block + (int64_t)li * kV;
 
@@ -483,8 +505,8 @@ int build_slot(int slot, const FastParams& p, hipStream_t st) {
 }
 
 template <class T, int M, int L2B, int S>
-int launch_fast(const void* x, void* y, void* l1, void* l2i, void* sch, void* codes, int64_t nb, int slot,
-                const FastParams& p, int dev, hipStream_t st) {
+int launch_fast(const void* x, void* y, void* l1, void* l2i, void* sch, void* codes, int64_t nb, int64_t causal_t,
+                int slot, const FastParams& p, int dev, hipStream_t st) {
     constexpr int lpb_log2 = 3;
     using St = typename T::storage;
     const size_t lds = (size_t)S * (p.n + 2) * 4 +
@@ -495,23 +517,28 @@ int launch_fast(const void* x, void* y, void* l1, void* l2i, void* sch, void* co
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kThreads, lds) != hipSuccess || per_cu <= 0)
         return 0;
     const int64_t blocks_per_wg = kThreads >> lpb_log2;
-    const int64_t ntiles = (nb + blocks_per_wg - 1) / blocks_per_wg;
+    int64_t ntiles = (nb + blocks_per_wg - 1) / blocks_per_wg;
+    if (causal_t) {   // wave units on or below the diagonal, kThreads / 64 a workgroup
+        const int64_t nbt = causal_t / 128, units = nb / (causal_t * nbt) * 8 * nbt * (nbt + 1);
+        ntiles = (units + kThreads / 64 - 1) / (kThreads / 64);
+    }
     // as many rounds as the resident workgroups need, with the tiles spread evenly over
     // them (a last round with few tiles would leave most of the chip idle)
     const int64_t resident = (int64_t)g_cus[dev] * per_cu;
     const int64_t rounds = (ntiles + resident - 1) / resident;
     const int64_t grid = (ntiles + rounds - 1) / rounds;
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), lds, st, (const St*)x, (St*)y, (St*)l1,
-                       (uint8_t*)l2i, (uint8_t*)sch, (uint8_t*)codes, nb, slot, p);
+                       (uint8_t*)l2i, (uint8_t*)sch, (uint8_t*)codes, nb, causal_t, slot, p);
     return 1;
 }
 
 template <class T, int M>
 int fast_by_shape(int l2b, int S, const void* x, void* y, void* l1, void* l2i, void* sch, void* codes, int64_t cols,
-                  int block, int lpb_log2, int64_t nb, int slot, const FastParams& p, int dev, hipStream_t st) {
+                  int block, int lpb_log2, int64_t nb, int64_t causal_t, int slot, const FastParams& p, int dev,
+                  hipStream_t st) {
 #define FAST_CASE(LB, SS)                                                                                   \
     if (l2b == LB && S == SS)                                                                               \
-        return launch_fast<T, M, LB, SS>(x, y, l1, l2i, sch, codes, nb, slot, p, dev, st);
+        return launch_fast<T, M, LB, SS>(x, y, l1, l2i, sch, codes, nb, causal_t, slot, p, dev, st);
     FAST_CASE(8, 1) FAST_CASE(8, 2) FAST_CASE(16, 1) FAST_CASE(16, 2) FAST_CASE(32, 1) FAST_CASE(32, 2)
 #undef FAST_CASE
     return 0;
@@ -524,7 +551,7 @@ using namespace hbq;
 
 int hbq_fast_try(const void* x, void* y, void* l1, void* l2i, void* sch, void* codes, int64_t rows, int64_t cols,
                  int dtype, int block, int mbit, int l2b, int l2_sc_bit, int scheme, const HbqParams& hp,
-                 hipStream_t st) {
+                 hipStream_t st, int64_t causal_t) {
     if (dtype != kF16 && dtype != kBF16) return 0;
     if (mbit < 1 || mbit > 3 || hp.J > kFastJ) return 0;
     if (l2b != 8 && l2b != 16 && l2b != 32) return 0;
@@ -600,9 +627,9 @@ int hbq_fast_try(const void* x, void* y, void* l1, void* l2i, void* sch, void* c
     const int lpb_log2 = lb - 4;
     int done;
 #define FAST_T(TT)                                                                                              \
-    (mbit == 1 ? fast_by_shape<TT, 1>(l2b, S, x, y, l1, l2i, sch, codes, cols, block, lpb_log2, nb, slot, p, dev, st) \
-     : mbit == 2 ? fast_by_shape<TT, 2>(l2b, S, x, y, l1, l2i, sch, codes, cols, block, lpb_log2, nb, slot, p, dev, st) \
-                 : fast_by_shape<TT, 3>(l2b, S, x, y, l1, l2i, sch, codes, cols, block, lpb_log2, nb, slot, p, dev, st))
+    (mbit == 1 ? fast_by_shape<TT, 1>(l2b, S, x, y, l1, l2i, sch, codes, cols, block, lpb_log2, nb, causal_t, slot, p, dev, st) \
+     : mbit == 2 ? fast_by_shape<TT, 2>(l2b, S, x, y, l1, l2i, sch, codes, cols, block, lpb_log2, nb, causal_t, slot, p, dev, st) \
+                 : fast_by_shape<TT, 3>(l2b, S, x, y, l1, l2i, sch, codes, cols, block, lpb_log2, nb, causal_t, slot, p, dev, st))
     done = dtype == kF16 ? FAST_T(F16) : FAST_T(BF16);
 #undef FAST_T
     return done;

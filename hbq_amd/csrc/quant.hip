@@ -513,11 +513,10 @@ int hbq_mxfp_qdq(const void* x, void* y, void* scales, void* codes, int64_t rows
     return hbq_check_launch("hbq_mxfp_qdq");
 }
 
-int hbq_hbq_qdq(const void* x, void* y, void* l1_scale, void* l2_index, void* scheme, void* codes, int64_t rows,
-                int64_t cols, int dtype, int block_size, int ebit, int mbit, int sc_ebit, int sc_mbit,
-                int l2_block_size, int l2_sc_bit, int l2_scheme, int scale_allow_subnormal, int use_ceil,
-                void* stream) {
-    hbq_clear_error();
+// argument checks and candidate tables shared by the HBQ entry points
+static int hbq_setup(HbqParams& p, int& S, Geometry& g, const void* x, const void* y, const void* codes, int64_t rows,
+                     int64_t cols, int dtype, int block_size, int ebit, int mbit, int sc_ebit, int sc_mbit,
+                     int l2_block_size, int l2_sc_bit, int l2_scheme, int scale_allow_subnormal, int use_ceil) {
     if (dtype != kF16 && dtype != kBF16 && dtype != kF32) return hbq_fail(HBQ_ERR_INVALID, "bad dtype code %d", dtype);
     if (ebit != 2) return hbq_fail(HBQ_ERR_UNSUPPORTED, "element exponent bits %d not supported on the GPU path", ebit);
     if (x == nullptr || y == nullptr) return hbq_fail(HBQ_ERR_INVALID, "null input/output pointer");
@@ -526,11 +525,9 @@ int hbq_hbq_qdq(const void* x, void* y, void* l1_scale, void* l2_index, void* sc
     if (l2_sc_bit < 0 || l2_sc_bit > 3)
         return hbq_fail(HBQ_ERR_UNSUPPORTED, "l2_sc_bit %d not supported on the GPU path (0..3)", l2_sc_bit);
     int esize = dtype == kF32 ? 4 : 2;
-    Geometry g;
     if (int rc = geometry(g, x, y, codes, rows, cols, block_size, esize)) return rc;
     if (l2_block_size > block_size) return hbq_fail(HBQ_ERR_INVALID, "l2_block_size larger than block_size");
-    HbqParams p{};
-    int S = 1;
+    S = 1;
     if (int rc = hbq_l2_table(p, S, l2_sc_bit, l2_scheme, dtype)) return rc;
     const int J = p.J;
     float elemax = round_host(max_norm_h(ebit, mbit), dtype);
@@ -539,7 +536,20 @@ int hbq_hbq_qdq(const void* x, void* y, void* l1_scale, void* l2_index, void* sc
         for (int j = 1; j < J; ++j) m = p.l2[j][s] > m ? p.l2[j][s] : m;
         p.em[s] = round_host((double)elemax * (double)m, dtype);
     }
-    if (int rc = scale_fmt(p.sf, sc_ebit, sc_mbit, scale_allow_subnormal, use_ceil)) return rc;
+    return scale_fmt(p.sf, sc_ebit, sc_mbit, scale_allow_subnormal, use_ceil);
+}
+
+int hbq_hbq_qdq(const void* x, void* y, void* l1_scale, void* l2_index, void* scheme, void* codes, int64_t rows,
+                int64_t cols, int dtype, int block_size, int ebit, int mbit, int sc_ebit, int sc_mbit,
+                int l2_block_size, int l2_sc_bit, int l2_scheme, int scale_allow_subnormal, int use_ceil,
+                void* stream) {
+    hbq_clear_error();
+    HbqParams p{};
+    int S = 1;
+    Geometry g;
+    if (int rc = hbq_setup(p, S, g, x, y, codes, rows, cols, dtype, block_size, ebit, mbit, sc_ebit, sc_mbit,
+                           l2_block_size, l2_sc_bit, l2_scheme, scale_allow_subnormal, use_ceil))
+        return rc;
     if (g.nb == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
     if (!g_hbq_force_generic) {
@@ -554,6 +564,30 @@ int hbq_hbq_qdq(const void* x, void* y, void* l1_scale, void* l2_index, void* sc
     else rc = dispatch_hbq<F32>(mbit, S, l2_block_size, g, x, y, l1_scale, l2_index, scheme, codes, cols, block_size, p, st);
     if (rc) return rc;
     return hbq_check_launch("hbq_hbq_qdq");
+}
+
+int hbq_hbq_qdq_causal(void* x, int64_t mats, int64_t t, int dtype, int block_size, int ebit, int mbit, int sc_ebit,
+                       int sc_mbit, int l2_block_size, int l2_sc_bit, int l2_scheme, int scale_allow_subnormal,
+                       int use_ceil, void* stream) {
+    hbq_clear_error();
+    if (mats < 0 || t < 0) return hbq_fail(HBQ_ERR_INVALID, "negative size");
+    if (t % 128 || block_size != 128)
+        return hbq_fail(HBQ_ERR_UNSUPPORTED, "the causal quantizer takes block_size 128 and t %% 128 == 0");
+    if (dtype != kF16 && dtype != kBF16) return hbq_fail(HBQ_ERR_UNSUPPORTED, "the causal quantizer takes fp16 / bf16");
+    HbqParams p{};
+    int S = 1;
+    Geometry g;
+    if (int rc = hbq_setup(p, S, g, x, x, nullptr, mats * t, t, dtype, block_size, ebit, mbit, sc_ebit, sc_mbit,
+                           l2_block_size, l2_sc_bit, l2_scheme, scale_allow_subnormal, use_ceil))
+        return rc;
+    if (g.nb == 0) return 0;
+    const int fr = g_hbq_force_generic ? 0
+                                       : hbq_fast_try(x, x, nullptr, nullptr, nullptr, nullptr, mats * t, t, dtype,
+                                                      block_size, mbit, l2_block_size, l2_sc_bit, l2_scheme, p,
+                                                      (hipStream_t)stream, t);
+    if (fr < 0) return -fr;
+    if (fr == 0) return hbq_fail(HBQ_ERR_UNSUPPORTED, "configuration outside the table kernel's");
+    return hbq_check_launch("hbq_hbq_qdq_causal");
 }
 
 int hbq_scale_quant(const void* x, void* y, int64_t n, int dtype, int ebit, int mbit, int allow_subnormal,

@@ -123,6 +123,26 @@ def causal_softmax_(s, scale):
     return s
 
 
+def quantize_causal_(qz, p):
+    """qz.q(p) for causal attention weights p [..., T, T] whose entries above the diagonal
+    are +0: in place on the GPU, the blocks entirely above the diagonal (quantized to +0)
+    left untouched; otherwise qz.q(p)."""
+    from .quantizer import HBQQuantizer
+    T = p.shape[-1]
+    if (type(qz) is HBQQuantizer and not qz.keep_l2_scale and p.is_cuda and p.is_contiguous()
+            and p.dtype in (torch.float16, torch.bfloat16) and p.dim() >= 2 and p.shape[-2] == T and T % 128 == 0
+            and qz.block_size == 128):
+        rc = _lib.lib().hbq_hbq_qdq_causal(
+            _lib.ptr(p), p.numel() // (T * T), T, _lib.DTYPE_CODE[p.dtype], qz.block_size, qz.ebit, qz.mbit,
+            qz.sc_ebit, qz.sc_mbit, qz.l2_block_size, qz.l2_sc_bit, qz.L2_SCHEME.index(qz.l2_scheme),
+            int(qz.scale_allow_subnormal), int(qz.use_ceil), _lib.stream_of(p))
+        if rc == 0:
+            return p
+        if rc != _lib.ERR_UNSUPPORTED:
+            _lib.check(rc)
+    return qz.q(p)
+
+
 def _rope_ok(x):
     return (x.is_cuda and x.dtype in (torch.float16, torch.bfloat16) and x.shape[-1] % 16 == 0
             and x.stride(-1) == 1 and all(st % 8 == 0 for st in x.stride()[:-1]) and x.data_ptr() % 16 == 0)
@@ -194,7 +214,7 @@ class QLlamaAttention(nn.Module):
                 s = s + torch.full((T, T), float("-inf"), device=q.device, dtype=s.dtype).triu(1)
             p = torch.softmax(s, dim=-1)
         if self.quant_attn_wgt:
-            p = self.attn_wgt_quantizer.q(p)
+            p = quantize_causal_(self.attn_wgt_quantizer, p)
         return torch.matmul(p.view(b, kvh, (H // kvh) * T, T), v).view(b, H, T, d), p
 
     def forward(self, x, cos, sin):

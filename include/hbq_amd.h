@@ -89,6 +89,17 @@ int hbq_hbq_qdq(const void *x, void *y, void *l1_scale, void *l2_index, void *sc
                 int l2_block_size, int l2_sc_bit, int l2_scheme, int scale_allow_subnormal, int use_ceil,
                 void *stream);
 
+/* The attention-weight quantizer of the causal manual attention (src/module.py:113-116,
+ * HBQQuantizer.q on the softmax output) in place on x [mats, t, t] (fp16 / bf16,
+ * t % 128 == 0, block_size 128), with the arguments of hbq_hbq_qdq.  The blocks
+ * entirely above the diagonal must hold +0 (the causal softmax gives exactly that);
+ * their quantization is +0, so they are left as they are and never read.  Returns
+ * HBQ_ERR_UNSUPPORTED for configurations outside the table kernel's (the caller
+ * then uses hbq_hbq_qdq). */
+int hbq_hbq_qdq_causal(void *x, int64_t mats, int64_t t, int dtype, int block_size, int ebit, int mbit, int sc_ebit,
+                       int sc_mbit, int l2_block_size, int l2_sc_bit, int l2_scheme, int scale_allow_subnormal,
+                       int use_ceil, void *stream);
+
 /*
  * Packed HBQ tensors (no reference counterpart in src/: the bit layout of the
  * HBQ hardware quantizer's outputs, hardware/HBQ_accelerator/hbq_e_quantizer/

@@ -53,9 +53,22 @@ def test_quantization_points_match_oracle(gpu, oracle):
                     return y
                 qz.q = rec
                 qz._wrapped = True
+    # the attention weights go through the in-place causal quantizer, not qz.q
+    import hbq_amd.llama as L
+    orig_causal = L.quantize_causal_
+
+    def rec_causal(qz, p):
+        x = p.detach().clone()
+        y = orig_causal(qz, p)
+        calls.append((qz, x, y.detach().clone()))
+        return y
+    L.quantize_causal_ = rec_causal
     ids = torch.randint(0, TINY.vocab_size, (1, 128), device=gpu)
-    with torch.no_grad():
-        out = m(ids)
+    try:
+        with torch.no_grad():
+            out = m(ids)
+    finally:
+        L.quantize_causal_ = orig_causal
     assert torch.isfinite(out).all()
     kinds = set()
     for qz, x, y in calls:
@@ -324,3 +337,26 @@ def test_silu_mul_matches_torch(gpu, dt):
     ref = torch.nn.functional.silu(gate) * up
     same = got.view(torch.int16) == ref.view(torch.int16)
     assert bool(same.all()), int((~same).sum())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_causal_quantizer_equals_full(gpu, dt):
+    """The in-place attention-weight quantizer that never touches the blocks above the
+    diagonal gives qz.q(p) bit for bit on causal softmax outputs (HBQ-A act, HBQ-E act and
+    a Mix weight configuration)."""
+    from hbq_amd.llama import causal_softmax_, quantize_causal_
+    g = torch.Generator(device=gpu).manual_seed(8)
+    qzs = [Q.HBQQuantizer(block_size=128, ebit=2, mbit=2, l2_block_size=8, l2_sc_bit=2, l2_scheme="SIG-1"),
+           Q.HBQQuantizer(block_size=128, ebit=2, mbit=2, l2_block_size=32, l2_sc_bit=2, l2_scheme="SIG-1"),
+           Q.HBQQuantizer(block_size=128, ebit=2, mbit=1, l2_block_size=8, l2_sc_bit=2, l2_scheme="Mix")]
+    for T, mats in ((128, 5), (256, 3), (2048, 2)):
+        s = (torch.randn(mats, T, T, device=gpu, generator=g) * 8).to(dt)
+        p = causal_softmax_(s, 0.088)
+        for qz in qzs:
+            ref = qz.q(p)
+            pin = p.clone()
+            got = quantize_causal_(qz, pin)
+            assert got is pin                   # the in-place kernel ran
+            same = got.view(torch.int16) == ref.view(torch.int16)
+            assert bool(same.all()), (T, qz.l2_scheme, qz.l2_block_size, int((~same).sum()))
