@@ -141,11 +141,17 @@ __global__ void build_lut_kernel(int slot, FastParams p) {
     }
 }
 
+// Workgroup size: the fp16 level table (1024 words a binade) takes 37 KB of LDS,
+// which 256-thread workgroups would replicate down to 3 waves a SIMD; 512 threads
+// share one copy between 8 waves.  The bf16 table is 8 times smaller.
+template <class T>
+constexpr int fast_threads() { return T::dt == kF16 ? 512 : 256; }
+
 // Block 128 (8 lanes x 16 elements).  Per-wave magnitude tables, laid out
 // [scheme][candidate][block-in-wave][level] with rows padded by one entry so
 // that the eight blocks of a wave fall on different LDS banks.
 template <class T, int M, int L2B, int S>
-__global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::storage* __restrict__ x,
+__global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typename T::storage* __restrict__ x,
                                                             typename T::storage* __restrict__ y,
                                                             typename T::storage* __restrict__ l1_out,
                                                             uint8_t* __restrict__ l2i_out,
@@ -161,12 +167,13 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
     constexpr int NSUBL = L2B <= kV ? kV / L2B : 1;
     constexpr int LPS = L2B <= kV ? 1 : L2B / kV;
     constexpr int SUBN = L2B <= kV ? L2B : kV;
-    constexpr int blocks_per_wg = kThreads / lpb;
+    constexpr int NTH = fast_threads<T>();
+    constexpr int blocks_per_wg = NTH / lpb;
     extern __shared__ uint32_t smem[];
     const int per = p.n + 2;
     uint32_t* lut = smem;
 
-    for (int i = threadIdx.x; i < S * per; i += kThreads) lut[i] = g_lut[slot][i];
+    for (int i = threadIdx.x; i < S * per; i += NTH) lut[i] = g_lut[slot][i];
     const int li = (int)(threadIdx.x & (lpb - 1));
     const int lane = (int)(threadIdx.x & 63);
     const int lane_base = lane - li;
@@ -200,8 +207,8 @@ __global__ __launch_bounds__(kThreads) void hbq_fast_kernel(const typename T::st
     const int64_t per_mat = 8 * nbt * (nbt + 1);
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int64_t nwork = causal_t ? nb / (causal_t * nbt) * per_mat : ntiles;
-    const int64_t first = causal_t ? (int64_t)blockIdx.x * (kThreads / 64) + wave : (int64_t)blockIdx.x;
-    const int64_t stride = causal_t ? (int64_t)gridDim.x * (kThreads / 64) : (int64_t)gridDim.x;
+    const int64_t first = causal_t ? (int64_t)blockIdx.x * (NTH / 64) + wave : (int64_t)blockIdx.x;
+    const int64_t stride = causal_t ? (int64_t)gridDim.x * (NTH / 64) : (int64_t)gridDim.x;
 
     for (int64_t tile = first; tile < nwork; tile += stride) {
         int64_t gb;
@@ -508,26 +515,27 @@ template <class T, int M, int L2B, int S>
 int launch_fast(const void* x, void* y, void* l1, void* l2i, void* sch, void* codes, int64_t nb, int64_t causal_t,
                 int slot, const FastParams& p, int dev, hipStream_t st) {
     constexpr int lpb_log2 = 3;
+    constexpr int NTH = fast_threads<T>();
     using St = typename T::storage;
     const size_t lds = (size_t)S * (p.n + 2) * 4 +
-                       (size_t)(kThreads >> lpb_log2) * S * kFastJ * ((1 << (M + 2)) + 1) * sizeof(DTabT<T>);
+                       (size_t)(NTH >> lpb_log2) * S * kFastJ * ((1 << (M + 2)) + 1) * sizeof(DTabT<T>);
     if (lds > 160 * 1024) return 0;
     auto kern = hbq_fast_kernel<T, M, L2B, S>;
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kThreads, lds) != hipSuccess || per_cu <= 0)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, NTH, lds) != hipSuccess || per_cu <= 0)
         return 0;
-    const int64_t blocks_per_wg = kThreads >> lpb_log2;
+    const int64_t blocks_per_wg = NTH >> lpb_log2;
     int64_t ntiles = (nb + blocks_per_wg - 1) / blocks_per_wg;
-    if (causal_t) {   // wave units on or below the diagonal, kThreads / 64 a workgroup
+    if (causal_t) {   // wave units on or below the diagonal, NTH / 64 a workgroup
         const int64_t nbt = causal_t / 128, units = nb / (causal_t * nbt) * 8 * nbt * (nbt + 1);
-        ntiles = (units + kThreads / 64 - 1) / (kThreads / 64);
+        ntiles = (units + NTH / 64 - 1) / (NTH / 64);
     }
     // as many rounds as the resident workgroups need, with the tiles spread evenly over
     // them (a last round with few tiles would leave most of the chip idle)
     const int64_t resident = (int64_t)g_cus[dev] * per_cu;
     const int64_t rounds = (ntiles + resident - 1) / resident;
     const int64_t grid = (ntiles + rounds - 1) / rounds;
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), lds, st, (const St*)x, (St*)y, (St*)l1,
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NTH), lds, st, (const St*)x, (St*)y, (St*)l1,
                        (uint8_t*)l2i, (uint8_t*)sch, (uint8_t*)codes, nb, causal_t, slot, p);
     return 1;
 }
