@@ -314,3 +314,38 @@ def test_hbq_causal_zero_blocks(gpu, oracle, name):
     finally:
         _lib.lib().hbq_set_generic_only(old)
     assert torch.equal(fast.codes, gen.codes)
+
+
+def test_quantizers_beyond_int32_offsets(gpu):
+    """Element offsets past 2^31 (the largest tensors a 288 GB device holds): rows at the
+    start, across the 2^31-element boundary and at the end quantize exactly as the same
+    rows alone, on the table kernels and the generic kernel (blocks are independent)."""
+    from hbq_amd import _lib
+    from hbq_amd.quantizer import HBQQuantizer, MXFPQuantizer
+    cols = 4096
+    b = (1 << 31) // cols
+    rows = b + 64
+    print(f"int64 offsets: {rows}x{cols} bf16", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(31)
+    x = torch.randn(rows, cols, device=gpu, dtype=torch.bfloat16, generator=g)
+    spans = [(0, 8), (b - 8, b + 8), (rows - 8, rows)]
+
+    def same_rows(qz, x, y):
+        for r0, r1 in spans:
+            alone = qz.q(x[r0:r1].clone())
+            assert torch.equal(y[r0:r1].view(torch.int16), alone.view(torch.int16)), (r0, r1)
+
+    hbq = HBQQuantizer(block_size=128, **HBQCFG["hbq_a_act"])
+    y = hbq.q(x)
+    same_rows(hbq, x, y)
+    old = _lib.lib().hbq_set_generic_only(1)
+    try:
+        y2 = hbq.q(x)
+    finally:
+        _lib.lib().hbq_set_generic_only(old)
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+    del y, y2
+    xh = x.half()
+    del x
+    mx = MXFPQuantizer(scale_allow_subnormal=False, **MXCFG["mxfp4"])
+    same_rows(mx, xh, mx.q(xh))
