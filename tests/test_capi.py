@@ -91,3 +91,30 @@ def test_packed_argument_errors_without_gpu(lib):
     # non-finite flag: bad stride
     rc = L.hbq_flag_nonfinite(fake, 4, 8, 4, 0, fake, None)
     assert rc == 1
+
+
+def test_decoder_kernel_argument_errors_without_gpu(lib):
+    """The decoder entry points (causal softmax, causal attention-weight quantizer, RMSNorm
+    halves, SiLU product) check their arguments before any HIP call; empty inputs are no-ops."""
+    from hbq_amd import _lib
+    L = _lib.lib()
+    fake = ctypes.c_void_p(256)
+    # causal softmax: t outside 64..2048 powers of two, bad dtype
+    assert L.hbq_causal_softmax(fake, fake, 2, 96, 1.0, 0, None) == 2
+    assert L.hbq_causal_softmax(fake, fake, 2, 128, 1.0, 2, None) == 2
+    assert L.hbq_causal_softmax(None, None, 0, 128, 1.0, 0, None) == 0
+    # causal quantizer: t % 128, block size, fp32, the quantizer's own checks (ebit)
+    args = (0, 128, 2, 2, 5, 3, 8, 2, 2, 0, 0, None)
+    assert L.hbq_hbq_qdq_causal(fake, 2, 192, *args) == 2
+    assert L.hbq_hbq_qdq_causal(fake, 2, 256, 0, 64, *args[2:]) == 2
+    assert L.hbq_hbq_qdq_causal(fake, 2, 256, 2, *args[1:]) == 2
+    assert L.hbq_hbq_qdq_causal(fake, 2, 256, 0, 128, 3, *args[3:]) == 2 and b"exponent" in L.hbq_last_error()
+    # RMSNorm halves and SiLU product: element counts and row lengths of 8, alignment, dtype
+    assert L.hbq_rms_prep(fake, None, None, fake, 12, 0, None) == 2
+    assert L.hbq_rms_prep(ctypes.c_void_p(258), None, None, fake, 16, 0, None) == 1
+    assert L.hbq_rms_prep(fake, fake, None, fake, 16, 0, None) == 1          # res without sum
+    assert L.hbq_rms_apply(fake, fake, fake, fake, 2, 12, 0, None) == 2
+    assert L.hbq_rms_apply(None, None, None, None, 0, 16, 0, None) == 0
+    assert L.hbq_silu_mul(fake, fake, fake, 16, 2, None) == 2
+    assert L.hbq_silu_mul(fake, fake, fake, 20, 0, None) == 2
+    assert L.hbq_silu_mul(None, None, None, 0, 1, None) == 0
