@@ -270,6 +270,8 @@ def test_causal_softmax_matches_torch(gpu, dt):
         s[0, 6, 9] = float("inf")            # masked +inf: inf - inf = NaN as well
         s[0, 7, 3] = -float("inf")
         s[1, 8, 1] = float("nan")
+        s[1, 3, 40] = float("nan")          # masked NaN: the whole row is NaN
+        s[1, 4, 50] = -float("inf")         # masked -inf: an ordinary masked row
         s[1, T - 1, :] = -6e4 if dt == torch.float16 else -3e38
         ref = s * scale
         ref = ref + torch.full((T, T), float("-inf"), device=gpu, dtype=dt).triu(1)
