@@ -434,13 +434,11 @@ __global__ __launch_bounds__(kThreads) void causal_softmax_kernel(const typename
     const int64_t i = row % Tn;
     const typename T::storage* src = s + row * Tn;
     float el[ITER];
-    bool bad = false;   // a masked score whose biased value is not -inf (scaled NaN or +inf)
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
         const int c = lane + 64 * it;
         const float scaled = T::round(T::load(src[c]) * scale);
         el[it] = T::round(scaled + (c > i ? -__builtin_inff() : 0.0f));
-        bad |= (c > i) & (el[it] != -__builtin_inff());
     }
     float mx = el[0];
 #pragma unroll
@@ -450,26 +448,18 @@ __global__ __launch_bounds__(kThreads) void causal_softmax_kernel(const typename
         const float b = __shfl_xor(mx, off, 64);
         mx = mx < b ? b : mx;
     }
-    // Chunks it > i / 64 lie wholly above the diagonal.  When the row's masked part is all
-    // -inf, each of their terms is exp(-inf - mx) = +0 (mx finite or +inf; mx = -inf or NaN
-    // makes the sum NaN through the unmasked terms anyway): adding +0 leaves the fp32 sum
-    // unchanged and each output is 0 / sum, so those chunks skip exp and the division.
-    const bool skip = !__builtin_amdgcn_ballot_w64(bad);
-    const int last = (int)(i >> 6);   // the chunk holding the diagonal
     float sum = 0.f;
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
-        if (skip && it > last) continue;
         el[it] = expf(el[it] - mx);
         sum += el[it];
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) sum = sum + __shfl_xor(sum, off, 64);
-    const float zq = sum == 0.f ? __builtin_nanf("") : 0.f / sum;
     typename T::storage* dst = p + row * Tn;
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
-        const float v = (skip && it > last) ? zq : (sum == 0.f ? __builtin_nanf("") : el[it] / sum);
+        const float v = sum == 0.f ? __builtin_nanf("") : el[it] / sum;
         dst[lane + 64 * it] = (T::dt == kBF16 && v != v) ? (typename T::storage)0x7FC0u : T::store(v);
     }
 }
