@@ -396,6 +396,29 @@ int hbq_gemm_fp32_accum(const void* A, const void* B, void* C, int64_t M, int64_
     return hbq_check_launch("gemm_fp32_accum");
 }
 
+int64_t hbq_gemm_fp32_accum_workspace(int64_t M, int64_t N, int64_t K, int b_is_nk) {
+    if (!b_is_nk || M < 1 || N < 1 || K < 1 || M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return 0;
+    const int s = splitk_fp32_splits((int)M, (int)N, (int)K);
+    return s > 1 ? (int64_t)s * M * N * (int64_t)sizeof(float) : 0;
+}
+
+int hbq_gemm_fp32_accum_ws(const void* A, const void* B, void* C, void* ws, int64_t ws_bytes, int64_t M, int64_t N,
+                           int64_t K, int b_is_nk, void* stream) {
+    hbq_clear_error();
+    if (int rc = check_shapes(A, B, C, M, N, K)) return rc;
+    if (ws_bytes < 0) return hbq_fail(HBQ_ERR_INVALID, "negative workspace size");
+    hipStream_t st = (hipStream_t)stream;
+    if (M == 0 || N == 0) return 0;
+    if (K == 0) return zero_output(C, M, N, st);
+    const int64_t need = hbq_gemm_fp32_accum_workspace(M, N, K, b_is_nk);
+    if (need > 0 && ws != nullptr && ws_bytes >= need &&
+        launch_splitk_fp32(A, B, C, (float*)ws, (int)M, (int)N, (int)K, (int)(need / ((int64_t)sizeof(float) * M * N)),
+                           st))
+        return hbq_check_launch("gemm_fp32_accum (split K)");
+    launch_any<kFp32, 4>(A, B, C, nullptr, (int)M, (int)N, (int)K, (int)K, b_is_nk, st);
+    return hbq_check_launch("gemm_fp32_accum");
+}
+
 int hbq_gemm_fp16_accum(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int b_is_nk,
                         void* stream) {
     hbq_clear_error();
@@ -464,8 +487,9 @@ int hbq_transpose16(const void* src, void* dst, int64_t rows, int64_t cols, void
 int hbq_gemm_group_partials(const void* A, const void* B, void* P, int64_t M, int64_t N, int64_t K, int group_k,
                             int b_is_nk, void* stream) {
     hbq_clear_error();
-    if (group_k != 16 && group_k != 32 && group_k != 64 && group_k != 128 && group_k != 256)
-        return hbq_fail(HBQ_ERR_INVALID, "group_k must be one of {16,32,64,128,256}");
+    // the ops' group sizes, or any multiple of the 128x128 kernel's K stage (a split-K half)
+    if (group_k != 16 && group_k != 32 && (group_k < 64 || group_k % BK != 0))
+        return hbq_fail(HBQ_ERR_INVALID, "group_k must be 16, 32 or a multiple of %d", BK);
     if (int rc = check_shapes(A, B, P, M, N, K)) return rc;
     if (M == 0 || N == 0 || K == 0) return 0;
     hipStream_t st = (hipStream_t)stream;

@@ -10,4 +10,11 @@ namespace hbq_gemm {
 int launch_tile256(int mode, int gn, const void* A, const void* B, void* C, float* P, int M, int N, int K, int gk,
                    int b_is_nk, hipStream_t st);
 
+// Split K for fp32 accumulation: the number of K ranges worth running for this shape
+// (1: none), and the launch (splits x M x N fp32 partials in ws, then their sum in
+// split order rounded to fp16); returns 0 when the layout does not allow it.
+int splitk_fp32_splits(int M, int N, int K);
+int launch_splitk_fp32(const void* A, const void* W, void* C, float* ws, int M, int N, int K, int splits,
+                       hipStream_t st);
+
 }  // namespace hbq_gemm

@@ -48,7 +48,7 @@ __device__ __forceinline__ int swz(int row, int chunk) { return row * TK + 8 * s
 template <int MODE, int GN, bool SMALLG, int GS, int SPG, int TN>
 __global__ __launch_bounds__(NT, 1) void kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ W,
                                                 uint16_t* __restrict__ C, float* __restrict__ P, int M, int N, int K,
-                                                int gk, int tiles_m, int tiles_n) {
+                                                int gk, int tiles_m, int tiles_n, int splits) {
     constexpr int WSL = TN * TK;          // halfs of one W slice
     constexpr int NWN = TN / 64;          // waves across the tile's columns
     constexpr int WROWS = TM * NWN / 8;   // rows of one wave (128 or 64)
@@ -66,6 +66,15 @@ __global__ __launch_bounds__(NT, 1) void kernel(const uint16_t* __restrict__ A, 
     // ---- tile of this workgroup ----
     const int T = tiles_m * tiles_n;
     int u = blockIdx.x;
+    // split K (fp32 accumulation): workgroups [s T, (s + 1) T) take the s-th of `splits`
+    // equal K ranges and write their fp32 partial sums to P[s]
+    int split = 0;
+    if (MODE == kFp32 && splits > 1) {
+        split = u / T;
+        u -= split * T;
+        A += (int64_t)split * (K / splits);
+        W += (int64_t)split * (K / splits);
+    }
     if ((T & 7) == 0) u = (u & 7) * (T >> 3) + (u >> 3);
     const int band = 4 * tiles_n;
     const int first = (u / band) * 4;
@@ -86,7 +95,7 @@ __global__ __launch_bounds__(NT, 1) void kernel(const uint16_t* __restrict__ A, 
     uint32_t voff[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) voff[i] = (uint32_t)(((wave + 8 * i) * 8 + lrow) * K + 8 * lchunk) * 2u;
-    const int nkt = K / TK;
+    const int nkt = (MODE == kFp32 && splits > 1) ? K / splits / TK : K / TK;
     auto issue = [&](int kt, uint16_t* la, uint16_t* lw) __attribute__((always_inline)) {
         const int k0 = kt * TK;
         const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
@@ -212,6 +221,26 @@ __global__ __launch_bounds__(NT, 1) void kernel(const uint16_t* __restrict__ A, 
     }
 
     if constexpr (MODE == kPartial) return;
+    if constexpr (MODE == kFp32) {
+        if (splits > 1) {   // this K range's fp32 sums, 4 columns a store
+            float* Ps = P + (int64_t)split * M * N;
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < RB; ++j) {
+                    const int m = m0 + wm + 32 * j + (lane & 31);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int n = n0 + wn + 32 * i + 8 * q + 4 * (lane >> 5);
+                        if (m < M && n < N)
+                            *reinterpret_cast<float4*>(Ps + (int64_t)m * N + n) =
+                                make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                            acc[i][j][4 * q + 3]);
+                    }
+                }
+            return;
+        }
+    }
 
     // ---- store: each wave stages its WROWS x 64 fp16 sub-tile in LDS, then writes full row segments ----
     static_assert(8 * WROWS * 64 <= 2 * SLICE + 2 * WSL, "staging area");
@@ -247,12 +276,13 @@ __global__ __launch_bounds__(NT, 1) void kernel(const uint16_t* __restrict__ A, 
 }
 
 template <int MODE, int GN, int TN>
-void launch(const void* A, const void* W, void* C, float* P, int M, int N, int K, int gk, hipStream_t st) {
+void launch(const void* A, const void* W, void* C, float* P, int M, int N, int K, int gk, hipStream_t st,
+            int splits = 1) {
     const int tm = (M + TM - 1) / TM, tn = (N + TN - 1) / TN;
-    const dim3 grid(tm * tn), block(NT);
+    const dim3 grid(tm * tn * splits), block(NT);
 #define T256_LAUNCH(SM, GS_, SPG_)                                                                              \
     hipLaunchKernelGGL((kernel<MODE, GN, SM, GS_, SPG_, TN>), grid, block, 0, st, (const uint16_t*)A,          \
-                       (const uint16_t*)W, (uint16_t*)C, P, M, N, K, gk, tm, tn)
+                       (const uint16_t*)W, (uint16_t*)C, P, M, N, K, gk, tm, tn, splits)
     if constexpr (MODE == kFp32) {
         T256_LAUNCH(false, 4, 1);
     } else {
@@ -293,6 +323,68 @@ static int launch_w(int mode, int gn, const void* A, const void* B, void* C, flo
     return 0;
 }
 
+namespace {
+
+int cu_count() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+            cus = n;
+    }
+    return cus;
+}
+
+// C = R16(P[0] + P[1] + ...) in split order, 8 outputs a thread (M * N % 8 == 0)
+__global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict__ P, uint16_t* __restrict__ C,
+                                                         int64_t mn, int splits) {
+    const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (u * 8 >= mn) return;
+    float v[8];
+    const float4* p0 = reinterpret_cast<const float4*>(P + 8 * u);
+    const float4 a = p0[0], b = p0[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    for (int s = 1; s < splits; ++s) {
+        const float4* ps = reinterpret_cast<const float4*>(P + (int64_t)s * mn + 8 * u);
+        const float4 c = ps[0], d = ps[1];
+        v[0] += c.x; v[1] += c.y; v[2] += c.z; v[3] += c.w; v[4] += d.x; v[5] += d.y; v[6] += d.z; v[7] += d.w;
+    }
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) w[q] = __builtin_bit_cast(uint32_t, cvt2(v[2 * q], v[2 * q + 1]));
+    *reinterpret_cast<uint4*>(C + 8 * u) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+}  // namespace
+
+int splitk_fp32_splits(int M, int N, int K) {
+    using namespace t256;
+    const int cus = cu_count();
+    if (cus <= 0 || M < 1 || N % 8 != 0 || K % (2 * TK) != 0) return 1;
+    if ((int64_t)M * K >= (1ll << 31) || (int64_t)N * K >= (1ll << 31)) return 1;
+    const int64_t tm = (M + TM - 1) / TM;
+    const int64_t t256 = tm * ((N + 255) / 256), t128 = tm * ((N + 127) / 128);
+    // long K on a grid of at most one round of 256x128 tiles: two K halves on 256x256
+    // tiles fill the same round with the more efficient tile (prefill down projection,
+    // M = 2048, K = 14336, N = 4096); the fp32 partials cost 2 x 2 x M x N x 4 bytes of traffic,
+    // which shorter K does not repay
+    if (t128 <= cus && 2 * t256 <= cus && K >= 8192) return 2;
+    return 1;
+}
+
+int launch_splitk_fp32(const void* A, const void* W, void* C, float* ws, int M, int N, int K, int splits,
+                       hipStream_t st) {
+    using namespace t256;
+    if (splits < 2 || (K / splits) % TK != 0) return 0;
+    if (((uintptr_t)A | (uintptr_t)W | (uintptr_t)C | (uintptr_t)ws) % 16 != 0) return 0;
+    launch<kFp32, 4, 256>(A, W, nullptr, ws, M, N, K, K / splits, st, splits);
+    const int64_t mn = (int64_t)M * N;
+    hipLaunchKernelGGL(splitk_sum_kernel, dim3((unsigned)((mn / 8 + 255) / 256)), dim3(256), 0, st, ws,
+                       (uint16_t*)C, mn, splits);
+    return 1;
+}
+
 int launch_tile256(int mode, int gn, const void* A, const void* B, void* C, float* P, int M, int N, int K, int gk,
                    int b_is_nk, hipStream_t st) {
     using namespace t256;
@@ -305,13 +397,7 @@ int launch_tile256(int mode, int gn, const void* A, const void* B, void* C, floa
     if (mode == kFp32) gk = K;
     // fewer 256x256 tiles than compute units would leave most of the chip idle: the
     // 128x128 kernel fills it better
-    static int cus = 0;
-    if (cus == 0) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
-            cus = n;
-    }
+    const int cus = cu_count();
     const int64_t tm = (M + TM - 1) / TM;
     // psum-quantized modes: 256x128 tiles when 256x256 tiles leave a partly empty last
     // round that 256x128 tiles fill (configs[2] gate/up: 896 tiles = 3.5 rounds against

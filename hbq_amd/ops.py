@@ -51,7 +51,7 @@ class FP32AccumMatMul(nn.Module):
     F.linear (cuBLAS).  This operator puts those linears on the same MFMA kernel as
     the other accumulation modes (x [.., K] fp16 against W [N, K], bias added in
     fp16); the fp32 sum order inside a K range differs from any library's, as it
-    does between libraries."""
+    does between libraries, and long K may be summed as two halves (split K)."""
 
     def forward(self, x, w, bias=None) -> torch.Tensor:
         orig_shape = x.shape
@@ -59,7 +59,7 @@ class FP32AccumMatMul(nn.Module):
         if x2d.dtype != torch.float16:
             x2d = x2d.half()
         w16 = w if w.dtype == torch.float16 else w.half()
-        out2d = ext.gemm_fp32_accum_nk(x2d, w16)
+        out2d = ext.gemm_fp32_accum_nk_split(x2d, w16)
         if bias is not None:
             out2d = out2d + bias
         return out2d.view(*orig_shape[:-1], -1)

@@ -178,6 +178,18 @@ int hbq_scale_quant(const void *x, void *y, int64_t n, int dtype, int ebit, int 
 int hbq_gemm_fp32_accum(const void *A, const void *B, void *C, int64_t M, int64_t N, int64_t K, int b_is_nk,
                         void *stream);
 
+/* gemm_fp32_accum with a caller-provided workspace (no reference counterpart: the
+ * reference's fp32-accumulation linears run F.linear, whose sum order is the
+ * library's).  For long K on grids of at most one round of tiles (the prefill's
+ * down projection) it splits K in halves over twice the workgroups, writes their fp32
+ * partial sums to ws and adds them in order before the single fp16 rounding; other
+ * shapes, or ws_bytes below hbq_gemm_fp32_accum_workspace(), run hbq_gemm_fp32_accum.
+ * The result of each half is the group partial hbq_gemm_group_partials gives for
+ * group_k = K / 2. */
+int64_t hbq_gemm_fp32_accum_workspace(int64_t M, int64_t N, int64_t K, int b_is_nk);
+int hbq_gemm_fp32_accum_ws(const void *A, const void *B, void *C, void *ws, int64_t ws_bytes, int64_t M, int64_t N,
+                           int64_t K, int b_is_nk, void *stream);
+
 /* Replaces gemm_fp16_accum -> gemm_fp16_accum_cuda (blockquant_ext.cpp:31-39, gemm.cu:568-591):
  * one fused fp16 multiply-add per k in ascending order (bit-exact for any input). */
 int hbq_gemm_fp16_accum(const void *A, const void *B, void *C, int64_t M, int64_t N, int64_t K, int b_is_nk,
@@ -198,7 +210,8 @@ int hbq_gemm_blockquant_mxfp8(const void *A, const void *B, void *C, int64_t M, 
 
 /* No reference counterpart: writes the fp32 partial sum of every group_k-wide K
  * group, P[ceil(K/group_k), M, N], from the same MFMA accumulation as the GEMMs,
- * so a test can apply the reference epilogue to exactly the kernel's partials. */
+ * so a test can apply the reference epilogue to exactly the kernel's partials.
+ * group_k: 16, 32 or a multiple of 64 (a split-K half, for instance). */
 int hbq_gemm_group_partials(const void *A, const void *B, void *P, int64_t M, int64_t N, int64_t K, int group_k,
                             int b_is_nk, void *stream);
 

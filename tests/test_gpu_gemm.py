@@ -259,3 +259,33 @@ def test_large_tile_kernel_bit_identical(gpu, op, gk, gn, K, M):
     big = call(W, True)
     assert torch.isfinite(small.float()).all()
     assert torch.equal(small.view(torch.int16), big.view(torch.int16))
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 4096, 14336), (512, 2048, 8192)])
+def test_fp32_split_k_is_the_sum_of_the_two_halves(gpu, M, N, K):
+    """Split-K fp32 accumulation (the prefill's long-K linears): C = R16(P0 + P1) bit for
+    bit, P0 and P1 the kernels' own fp32 sums over the two K halves (group partials with
+    group_k = K / 2); and within fp32-accumulation tolerance of the unsplit GEMM."""
+    from hbq_amd import _lib, blockquant_ext as ext
+    print(f"split K {M}x{N}x{K}", flush=True)
+    assert _lib.lib().hbq_gemm_fp32_accum_workspace(M, N, K, 1) == 2 * M * N * 4
+    g = torch.Generator(device=gpu).manual_seed(M + K)
+    A = torch.randn(M, K, device=gpu, generator=g).half()
+    W = (torch.randn(N, K, device=gpu, generator=g) * 0.02).half()
+    C = ext.gemm_fp32_accum_nk_split(A, W)
+    P = ext.group_partials(A, W, K // 2, b_is_nk=True)
+    assert P.shape[0] == 2
+    ref = (P[0] + P[1]).half()
+    assert torch.equal(C.view(torch.int16), ref.view(torch.int16))
+    full = ext.gemm_fp32_accum_nk(A, W).float()
+    rel = ((C.float() - full).norm() / full.norm()).item()
+    assert rel < 1e-3, rel
+
+
+def test_fp32_split_k_only_for_long_k(gpu):
+    """Shapes that fill the chip, or short K, take no workspace (unsplit GEMM)."""
+    from hbq_amd import _lib
+    L = _lib.lib()
+    assert L.hbq_gemm_fp32_accum_workspace(2048, 4096, 4096, 1) == 0      # short K
+    assert L.hbq_gemm_fp32_accum_workspace(4096, 4096, 14336, 1) == 0     # more tiles than one round
+    assert L.hbq_gemm_fp32_accum_workspace(2048, 4096, 14336, 0) == 0     # B[K, N] layout
