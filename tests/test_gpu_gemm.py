@@ -289,3 +289,28 @@ def test_fp32_split_k_only_for_long_k(gpu):
     assert L.hbq_gemm_fp32_accum_workspace(2048, 4096, 4096, 1) == 0      # short K
     assert L.hbq_gemm_fp32_accum_workspace(4096, 4096, 14336, 1) == 0     # more tiles than one round
     assert L.hbq_gemm_fp32_accum_workspace(2048, 4096, 14336, 0) == 0     # B[K, N] layout
+
+
+@pytest.mark.parametrize("op,gk,gn", [("fp32", 0, 0), ("grouped", 128, 0), ("mxint8", 128, 32)])
+def test_wide_tiles_on_short_grids_bit_identical(gpu, op, gk, gn):
+    """M = 2000, N = 6144: 192 tiles of 256 x 256 (fewer than the compute units) run in one
+    round instead of two rounds of 384 narrower tiles (the prefill's q/k/v shape); the bits
+    equal the 128x128 kernel's on B[K, N]."""
+    from hbq_amd import blockquant_ext as ext
+    M, K, N = 2000, 512, 6144
+    print(f"wide tiles, short grid: {op}", flush=True)
+    A = synth(M, K, 61, "f16").to(gpu)
+    B = synth(K, N, 62, "f16", std=0.02).to(gpu)
+    W = B.t().contiguous()
+    call = {"fp32": lambda b, nk: ext.gemm_fp32_accum(A, b, b_is_nk=nk),
+            "grouped": lambda b, nk: ext.gemm_fp16_grouped_accum(A, b, gk, b_is_nk=nk),
+            "mxint8": lambda b, nk: ext.gemm_blockquant_mxint8(A, b, gk, gn, b_is_nk=nk)}[op]
+    old = ext.TRANSPOSE_MIN_MNK
+    try:
+        ext.TRANSPOSE_MIN_MNK = 1 << 62
+        small = call(B, False)
+    finally:
+        ext.TRANSPOSE_MIN_MNK = old
+    big = call(W, True)
+    assert torch.isfinite(small.float()).all()
+    assert torch.equal(small.view(torch.int16), big.view(torch.int16))
