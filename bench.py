@@ -389,7 +389,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the HBQ hot path here has no multi-GPU mode (--gpus {args.gpus} "
-              f"requested). The quantizer and GEMM shard without communication; see DESIGN.md.", file=sys.stderr)
+              f"requested). The quantizer shards by rows and the GEMMs by N or M, without communication.",
+              file=sys.stderr)
         sys.exit(2)
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
