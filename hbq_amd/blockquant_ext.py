@@ -112,15 +112,17 @@ _WORKSPACE = {}
 def gemm_fp32_accum_nk_split(A, W):
     """gemm_fp32_accum_nk that may split K: for long K on grids of at most one round of
     tiles it sums two K halves' fp32 partials (each the kernel's own group partial for
-    group_k = K / 2) before the fp16 rounding; the split-K workspace is cached per device
-    and reused on the stream.  Same fp32-accumulation contract, another summation order."""
+    group_k = K / 2) before the fp16 rounding.  The split-K workspace is cached per device
+    and stream (calls on one stream run in order, so they can share it).  Same
+    fp32-accumulation contract, another summation order."""
     A, W, C, M, N, K, _ = _prep(A, W, True)
     need = _lib.lib().hbq_gemm_fp32_accum_workspace(M, N, K, 1)
     ws = None
     if need > 0:
-        ws = _WORKSPACE.get(A.device)
+        key = (A.device, torch.cuda.current_stream(A.device).cuda_stream)
+        ws = _WORKSPACE.get(key)
         if ws is None or ws.numel() * 4 < need:
-            ws = _WORKSPACE[A.device] = torch.empty((need + 3) // 4, dtype=torch.float32, device=A.device)
+            ws = _WORKSPACE[key] = torch.empty((need + 3) // 4, dtype=torch.float32, device=A.device)
     _call(_lib.lib().hbq_gemm_fp32_accum_ws, _lib.ptr(A), _lib.ptr(W), _lib.ptr(C), _lib.ptr(ws),
           ws.numel() * 4 if ws is not None else 0, M, N, K, 1, _lib.stream_of(A))
     return C
