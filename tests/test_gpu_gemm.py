@@ -261,7 +261,7 @@ def test_large_tile_kernel_bit_identical(gpu, op, gk, gn, K, M):
     assert torch.equal(small.view(torch.int16), big.view(torch.int16))
 
 
-@pytest.mark.parametrize("M,N,K", [(2048, 4096, 14336), (512, 2048, 8192)])
+@pytest.mark.parametrize("M,N,K", [(2048, 4096, 14336), (512, 2048, 8192), (300, 1000, 8192)])
 def test_fp32_split_k_is_the_sum_of_the_two_halves(gpu, M, N, K):
     """Split-K fp32 accumulation (the prefill's long-K linears): C = R16(P0 + P1) bit for
     bit, P0 and P1 the kernels' own fp32 sums over the two K halves (group partials with
