@@ -433,11 +433,26 @@ __global__ __launch_bounds__(kThreads) void causal_softmax_kernel(const typename
     const int lane = threadIdx.x & 63;
     const int64_t i = row % Tn;
     const typename T::storage* src = s + row * Tn;
+    // rows of 512 or more: 16-byte global loads and stores staged through this wave's LDS
+    // row, from which each lane takes its columns lane + 64 it (the reduction order)
+    constexpr bool STAGE = ITER >= 8;
+    __shared__ __attribute__((aligned(16))) uint16_t rowbuf[STAGE ? kThreads / 64 : 1][STAGE ? Tn : 8];
+    uint16_t* rb = rowbuf[STAGE ? (threadIdx.x >> 6) : 0];
+    if constexpr (STAGE) {
+#pragma unroll
+        for (int q = 0; q < ITER / 8; ++q) {
+            const int c8 = 8 * (lane + 64 * q);
+            *reinterpret_cast<u32x4*>(rb + c8) = *reinterpret_cast<const u32x4*>(src + c8);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
     float el[ITER];
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
         const int c = lane + 64 * it;
-        const float scaled = T::round(T::load(src[c]) * scale);
+        const float scaled = T::round(T::load(STAGE ? rb[c] : src[c]) * scale);
         el[it] = T::round(scaled + (c > i ? -__builtin_inff() : 0.0f));
     }
     float mx = el[0];
@@ -460,7 +475,19 @@ __global__ __launch_bounds__(kThreads) void causal_softmax_kernel(const typename
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
         const float v = sum == 0.f ? __builtin_nanf("") : el[it] / sum;
-        dst[lane + 64 * it] = (T::dt == kBF16 && v != v) ? (typename T::storage)0x7FC0u : T::store(v);
+        const typename T::storage o = (T::dt == kBF16 && v != v) ? (typename T::storage)0x7FC0u : T::store(v);
+        if constexpr (STAGE) rb[lane + 64 * it] = o;
+        else dst[lane + 64 * it] = o;
+    }
+    if constexpr (STAGE) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int q = 0; q < ITER / 8; ++q) {
+            const int c8 = 8 * (lane + 64 * q);
+            *reinterpret_cast<u32x4*>(dst + c8) = *reinterpret_cast<const u32x4*>(rb + c8);
+        }
     }
 }
 
@@ -672,6 +699,7 @@ int hbq_causal_softmax(const void* s, void* p, int64_t mats, int64_t t, double s
         return hbq_fail(HBQ_ERR_UNSUPPORTED, "the fused causal softmax takes t = 64, 128, ..., 2048");
     if (mats == 0) return 0;
     if (!s || !p) return hbq_fail(HBQ_ERR_INVALID, "null pointer");
+    if (((uintptr_t)s | (uintptr_t)p) % 16) return hbq_fail(HBQ_ERR_INVALID, "scores must be 16-byte aligned");
     const int64_t rows = mats * t;
     const int64_t grid = (rows + (kThreads / 64) - 1) / (kThreads / 64);
     if (grid > 0x7fffffff) return hbq_fail(HBQ_ERR_INVALID, "tensor too large");

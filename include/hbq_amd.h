@@ -236,7 +236,8 @@ int hbq_scale_causal_mask(void *s, int64_t mats, int64_t t, double scale, int dt
  * torch.softmax along the rows (src/module.py:96-113), one pass over the scores.  The
  * softmax repeats torch's persistent warp softmax step for step (row max and sum per
  * 64-lane wave in its element order and butterfly order, exp, division), so p has
- * torch's bits.  [mats, t, t] fp16 / bf16 with t a power of two from 64 to 2048. */
+ * torch's bits.  [mats, t, t] fp16 / bf16 with t a power of two from 64 to 2048,
+ * 16-byte aligned. */
 int hbq_causal_softmax(const void *s, void *p, int64_t mats, int64_t t, double scale, int dtype, void *stream);
 
 /* Rotary embedding of the decoder's q or k (no counterpart kernel: the elementwise
