@@ -419,6 +419,27 @@ int hbq_gemm_fp32_accum_ws(const void* A, const void* B, void* C, void* ws, int6
     return hbq_check_launch("gemm_fp32_accum");
 }
 
+int hbq_gemm_fp32_accum_batched(const void* A, const void* W, void* C, int64_t batches, int64_t M, int64_t N,
+                                int64_t K, int64_t stride_a, int64_t stride_w, int64_t stride_c, void* stream) {
+    hbq_clear_error();
+    if (batches < 0) return hbq_fail(HBQ_ERR_INVALID, "negative batch count");
+    if (int rc = check_shapes(A, W, C, M, N, K)) return rc;
+    if (batches > 65535) return hbq_fail(HBQ_ERR_INVALID, "too many batches");
+    if (stride_a < M * K || stride_w < N * K || stride_c < M * N)
+        return hbq_fail(HBQ_ERR_INVALID, "batch strides smaller than one problem");
+    hipStream_t st = (hipStream_t)stream;
+    if (batches == 0 || M == 0 || N == 0) return 0;
+    if (K == 0) {
+        for (int64_t z = 0; z < batches; ++z) zero_output((uint16_t*)C + z * stride_c, M, N, st);
+        return hbq_check_launch("gemm_fp32_accum_batched");
+    }
+    if (!launch_batched_fp32(A, W, C, (int)batches, (int)M, (int)N, (int)K, stride_a, stride_w, stride_c, st))
+        for (int64_t z = 0; z < batches; ++z)
+            launch_any<kFp32, 4>((const uint16_t*)A + z * stride_a, (const uint16_t*)W + z * stride_w,
+                                 (uint16_t*)C + z * stride_c, nullptr, (int)M, (int)N, (int)K, (int)K, 1, st);
+    return hbq_check_launch("gemm_fp32_accum_batched");
+}
+
 int hbq_gemm_fp16_accum(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int b_is_nk,
                         void* stream) {
     hbq_clear_error();

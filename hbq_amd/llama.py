@@ -143,6 +143,25 @@ def quantize_causal_(qz, p):
     return qz.q(p)
 
 
+def _batched_gemm_ok(a, w, vT):
+    """Both attention products fit hbq_gemm_fp32_accum_batched: fp16 on the GPU, K of
+    each product (head_dim, tokens) a multiple of 64, contiguous operands."""
+    d, T = a.shape[-1], w.shape[-2]
+    return (a.is_cuda and a.dtype == torch.float16 and w.dtype == torch.float16 and vT.dtype == torch.float16
+            and a.is_contiguous() and w.is_contiguous() and vT.is_contiguous() and d % 64 == 0 and T % 64 == 0)
+
+
+def _batched_gemm(a, w):
+    """C[..., M, N] = a[..., M, K] @ w[..., N, K]^T in fp32 accumulation, one HIP launch
+    over the leading dims (the same arithmetic as the fp32-accumulation linears)."""
+    M, K, N = a.shape[-2], a.shape[-1], w.shape[-2]
+    Z = a.numel() // (M * K)
+    c = torch.empty(a.shape[:-1] + (N,), dtype=torch.float16, device=a.device)
+    _lib.check(_lib.lib().hbq_gemm_fp32_accum_batched(_lib.ptr(a), _lib.ptr(w), _lib.ptr(c), Z, M, N, K, M * K,
+                                                      N * K, M * N, _lib.stream_of(a)))
+    return c
+
+
 def _rope_ok(x):
     return (x.is_cuda and x.dtype in (torch.float16, torch.bfloat16) and x.shape[-1] % 16 == 0
             and x.stride(-1) == 1 and all(st % 8 == 0 for st in x.stride()[:-1]) and x.data_ptr() % 16 == 0)
@@ -192,17 +211,25 @@ class QLlamaAttention(nn.Module):
         # one GEMM over the stacked q/k/v weights when their operators allow it (same bits)
         self.stack_qkv = False
 
-    def manual_sdpa(self, q, k, v):
+    def manual_sdpa(self, q, k, v, vT=None):
         """Causal softmax(q k^T / sqrt(d)) v with the attention weights quantized after the
         softmax (src/module.py:93-117).  q [b, H, T, d]; k, v [b, KVH, T, d] with the query
         heads of one kv head consecutive (repeat_kv's order): each kv head's rep = H / KVH
         query heads multiply it as one [rep * T, d] operand, which reads the same scores and
-        outputs as the repeated k and v without copying them."""
+        outputs as the repeated k and v without copying them.  With vT = v^T [b, KVH, d, T]
+        contiguous (and v None) on the GPU, both products run on the HIP fp32-accumulation
+        GEMM, batched over the kv heads: k and vT are its W[N, K] operands as they lie."""
         b, H, T, d = q.shape
         kvh = k.shape[1]
         scale = 1.0 / math.sqrt(d)
         qg = q.reshape(b, kvh, (H // kvh) * T, d)
-        s = torch.matmul(qg, k.transpose(-2, -1).contiguous()).view(b, H, T, T)
+        if vT is not None and _batched_gemm_ok(qg, k, vT):
+            s = _batched_gemm(qg, k).view(b, H, T, T)
+        else:
+            if v is None:
+                v = vT.transpose(-1, -2).contiguous()
+                vT = None
+            s = torch.matmul(qg, k.transpose(-2, -1).contiguous()).view(b, H, T, T)
         fused = s.is_cuda and s.dtype in (torch.float16, torch.bfloat16) and s.is_contiguous() and s.shape[-1] == T
         if fused and T in (64, 128, 256, 512, 1024, 2048):
             p = causal_softmax_(s, scale)           # * scale, + the causal bias and softmax: one HIP pass
@@ -215,7 +242,9 @@ class QLlamaAttention(nn.Module):
             p = torch.softmax(s, dim=-1)
         if self.quant_attn_wgt:
             p = quantize_causal_(self.attn_wgt_quantizer, p)
-        return torch.matmul(p.view(b, kvh, (H // kvh) * T, T), v).view(b, H, T, d), p
+        pg = p.view(b, kvh, (H // kvh) * T, T)
+        out = _batched_gemm(pg, vT) if vT is not None else torch.matmul(pg, v)
+        return out.view(b, H, T, d), p
 
     def forward(self, x, cos, sin):
         b, T, _ = x.shape
@@ -242,10 +271,11 @@ class QLlamaAttention(nn.Module):
             q = self.q_proj.aq.q(q)
         if self.quant_k_cache:
             k = self.kv_quantizer.q(k)                        # (batch, heads, tokens, head_dim)
+        # V^T, tokens last: V is quantized along the tokens (the following product is P @ V)
+        vT = v.transpose(-1, -2).contiguous()
         if self.quant_v_cache:
-            # V is quantized along the tokens: the following product is P @ V
-            v = self.kv_quantizer.q(v.transpose(-1, -2).contiguous()).transpose(-1, -2).contiguous()
-        out, _ = self.manual_sdpa(q.contiguous(), k.contiguous(), v.contiguous())
+            vT = self.kv_quantizer.q(vT)
+        out, _ = self.manual_sdpa(q.contiguous(), k.contiguous(), None, vT=vT)
         out = out.transpose(1, 2).contiguous().view(b, T, -1)
         return self.o_proj(out)
 

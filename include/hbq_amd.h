@@ -190,6 +190,14 @@ int64_t hbq_gemm_fp32_accum_workspace(int64_t M, int64_t N, int64_t K, int b_is_
 int hbq_gemm_fp32_accum_ws(const void *A, const void *B, void *C, void *ws, int64_t ws_bytes, int64_t M, int64_t N,
                            int64_t K, int b_is_nk, void *stream);
 
+/* No reference counterpart: `batches` independent fp32-accumulation GEMMs
+ * C_z[M,N] = A_z[M,K] W_z[N,K]^T (fp16, z-th problem at element offsets z * stride_*),
+ * the same arithmetic as hbq_gemm_fp32_accum with b_is_nk = 1, in one launch.  The
+ * decoder's attention products use it: q against k (W = k, no transpose) and the
+ * attention weights against the quantized V^T. */
+int hbq_gemm_fp32_accum_batched(const void *A, const void *W, void *C, int64_t batches, int64_t M, int64_t N,
+                                int64_t K, int64_t stride_a, int64_t stride_w, int64_t stride_c, void *stream);
+
 /* Replaces gemm_fp16_accum -> gemm_fp16_accum_cuda (blockquant_ext.cpp:31-39, gemm.cu:568-591):
  * one fused fp16 multiply-add per k in ascending order (bit-exact for any input). */
 int hbq_gemm_fp16_accum(const void *A, const void *B, void *C, int64_t M, int64_t N, int64_t K, int b_is_nk,

@@ -314,3 +314,20 @@ def test_wide_tiles_on_short_grids_bit_identical(gpu, op, gk, gn):
     big = call(W, True)
     assert torch.isfinite(small.float()).all()
     assert torch.equal(small.view(torch.int16), big.view(torch.int16))
+
+
+@pytest.mark.parametrize("Z,M,N,K", [(8, 8192, 2048, 128), (8, 8192, 128, 2048), (3, 300, 1000, 192)])
+def test_fp32_batched_equals_per_problem(gpu, Z, M, N, K):
+    """hbq_gemm_fp32_accum_batched (the decoder's attention products: q k^T and P V) gives
+    each problem the bits of gemm_fp32_accum on W[N, K] alone."""
+    from hbq_amd import _lib, blockquant_ext as ext
+    print(f"batched fp32 {Z}x{M}x{N}x{K}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(Z * M + N)
+    A = torch.randn(Z, M, K, device=gpu, generator=g).half()
+    W = (torch.randn(Z, N, K, device=gpu, generator=g) * 0.1).half()
+    C = torch.empty(Z, M, N, device=gpu, dtype=torch.float16)
+    _lib.check(_lib.lib().hbq_gemm_fp32_accum_batched(_lib.ptr(A), _lib.ptr(W), _lib.ptr(C), Z, M, N, K, M * K,
+                                                      N * K, M * N, _lib.stream_of(A)))
+    for z in range(Z):
+        ref = ext.gemm_fp32_accum_nk(A[z], W[z])
+        assert torch.equal(C[z].view(torch.int16), ref.view(torch.int16)), z

@@ -291,6 +291,8 @@ def test_grouped_query_attention_equals_repeated_kv_cpu():
     k = torch.randn(2, KVH, T, d)
     v = torch.randn(2, KVH, T, d)
     out, p = a.manual_sdpa(q, k, v)
+    out_t, _ = a.manual_sdpa(q, k, None, vT=v.transpose(-1, -2).contiguous())   # the V^T entry
+    torch.testing.assert_close(out_t, out, rtol=1e-6, atol=1e-6)
     kr, vr = k.repeat_interleave(H // KVH, dim=1), v.repeat_interleave(H // KVH, dim=1)
     s = q @ kr.transpose(-2, -1) / d ** 0.5 + torch.full((T, T), float("-inf")).triu(1)
     pr = torch.softmax(s, dim=-1)
