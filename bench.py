@@ -104,7 +104,7 @@ def hbq_launcher(x, cfg, codes=True):
     sc = torch.empty(rows, nblk, dtype=torch.uint8, device=x.device) if codes else None
     args = [_lib.ptr(x), _lib.ptr(y), _lib.ptr(l1), _lib.ptr(l2), _lib.ptr(sc), _lib.ptr(c), rows, cols,
             _lib.DTYPE_CODE[x.dtype], 128, cfg["ebit"], cfg["mbit"], 5, 3, cfg["l2_block_size"], cfg["l2_sc_bit"],
-            HBQQuantizer.L2_SCHEME.index(cfg["l2_scheme"]), 0, 0, _lib.stream_of(x)]
+            HBQQuantizer.L2_SCHEME.index(cfg["l2_scheme"]), 0, 0, 1, _lib.stream_of(x)]
     fn = L.hbq_hbq_qdq
 
     def step():
@@ -124,7 +124,7 @@ def mx_launcher(x, cfg, codes=True):
         if codes else None
     s = torch.empty(rows, cols // B, dtype=x.dtype, device=x.device) if codes else None
     args = [_lib.ptr(x), _lib.ptr(y), _lib.ptr(s), _lib.ptr(c), rows, cols, _lib.DTYPE_CODE[x.dtype], B, cfg["ebit"],
-            cfg["mbit"], cfg["sc_ebit"], cfg["sc_mbit"], 0, 0, 0, 0, 1.0, _lib.stream_of(x)]
+            cfg["mbit"], cfg["sc_ebit"], cfg["sc_mbit"], 0, 0, 0, 0, 1.0, 0, _lib.stream_of(x)]
     fn = L.hbq_mxfp_qdq
 
     def step():

@@ -20,9 +20,9 @@ SIGNATURES = {
     "hbq_last_error": ([], ctypes.c_char_p),
     "hbq_abi_version": ([], _I),
     "hbq_set_generic_only": ([_I], _I),
-    "hbq_mxfp_qdq": ([_P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _D, _P], _I),
-    "hbq_hbq_qdq": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
-    "hbq_elem_quant": ([_P, _P, _P, _I64, _I, _I, _I, _P], _I),
+    "hbq_mxfp_qdq": ([_P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _D, _I, _P], _I),
+    "hbq_hbq_qdq": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
+    "hbq_elem_quant": ([_P, _P, _P, _I64, _I, _I, _I, _I, _P], _I),
     "hbq_scale_quant": ([_P, _P, _I64, _I, _I, _I, _I, _I, _I, _P], _I),
     "hbq_gemm_fp32_accum_workspace": ([_I64, _I64, _I64, _I], _I64),
     "hbq_gemm_fp32_accum_ws": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P], _I),
@@ -37,7 +37,7 @@ SIGNATURES = {
     "hbq_flag_nonfinite": ([_P, _I64, _I64, _I64, _I, _P, _P], _I),
     "hbq_scale_causal_mask": ([_P, _I64, _I64, ctypes.c_double, _I, _P], _I),
     "hbq_causal_softmax": ([_P, _P, _I64, _I64, ctypes.c_double, _I, _P], _I),
-    "hbq_hbq_qdq_causal": ([_P, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
+    "hbq_hbq_qdq_causal": ([_P, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "hbq_rms_prep": ([_P, _P, _P, _P, _I64, _I, _P], _I),
     "hbq_rms_apply": ([_P, _P, _P, _P, _I64, _I64, _I, _P], _I),
     "hbq_silu_mul": ([_P, _P, _P, _I64, _I, _P], _I),

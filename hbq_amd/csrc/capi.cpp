@@ -27,6 +27,6 @@ extern "C" {
 
 const char* hbq_last_error(void) { return g_err; }
 
-int hbq_abi_version(void) { return 1; }
+int hbq_abi_version(void) { return 2; }
 
 }

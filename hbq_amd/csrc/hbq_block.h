@@ -47,7 +47,7 @@ __device__ __forceinline__ void hbq_block(const float* xv, int li, int lpb, int 
 #pragma unroll
             for (int i = 0; i < kV; ++i) {
                 float u = (l2 == 1.0f) ? t[i] : div_T<T>(t[i], l2, rl2);
-                float q = elem_quant<T, M>(u, cj[i]);
+                float q = elem_quant<T, M>(u, cj[i], p.fused);
                 float d = T::round(T::round(q * l2) * l1[s]);
                 float e = T::round(xv[i] - d);
                 dj[i] = d;

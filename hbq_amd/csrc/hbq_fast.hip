@@ -54,6 +54,7 @@ struct FastParams {
     float em[2];
     float rem[2];              // R32(1 / em): R_T(amax * rem) equals R_T(amax / em) wherever the clamp below keeps it
     int use_ceil;
+    int fused;                 // the table's element rounding: compiled lpfp_quant (1) or eager (0)
 };
 
 // fp16 tables hold halves (the candidate errors are computed in packed fp16),
@@ -84,9 +85,9 @@ __device__ __forceinline__ float from_bits(uint32_t b) {
 
 // magnitude code of the element quantizer = its level (exponent field and mantissa)
 template <class T, int M>
-__device__ __forceinline__ uint32_t level_of(float u) {
+__device__ __forceinline__ uint32_t level_of(float u, bool fused) {
     uint32_t c;
-    elem_quant<T, M>(u, c);
+    elem_quant<T, M>(u, c, fused);
     return c & ((1u << (M + 2)) - 1u);
 }
 
@@ -109,7 +110,8 @@ __global__ void build_lut_kernel(int slot, FastParams p) {
             for (int j = 0; j < p.J; ++j) w |= (((1u << (M + 2)) - 1u) * esize) << (8 * j);
         } else if (k > 0) {
             const float t = from_bits<T>(p.lo_bits + (uint32_t)(k - 1));
-            for (int j = 0; j < p.J; ++j) w |= (level_of<T, M>(T::round(t / p.l2[j][s])) * esize) << (8 * j);
+            for (int j = 0; j < p.J; ++j)
+                w |= (level_of<T, M>(T::round(t / p.l2[j][s]), p.fused) * esize) << (8 * j);
         }
         g_lut[slot][i] = w;
     }
@@ -127,8 +129,8 @@ __global__ void build_lut_kernel(int slot, FastParams p) {
         const float top = from_bits<T>(p.lo_bits + (uint32_t)p.n);
         for (int s = 0; s < p.S; ++s)
             for (int j = 0; j < p.J; ++j) {
-                if (level_of<T, M>(T::round(below / p.l2[j][s])) != 0) status = 1;
-                if (level_of<T, M>(T::round(top / p.l2[j][s])) != (1u << (M + 2)) - 1u) status = 2;
+                if (level_of<T, M>(T::round(below / p.l2[j][s]), p.fused) != 0) status = 1;
+                if (level_of<T, M>(T::round(top / p.l2[j][s]), p.fused) != (1u << (M + 2)) - 1u) status = 2;
                 float z = -1.f;
                 for (uint32_t b = 1; b < 4096 && z < 0.f; ++b) {
                     const float t = from_bits<T>(b);
@@ -485,9 +487,10 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
 namespace {
 
 struct LutKey {
-    int dtype, mbit, scheme, l2_sc_bit;
+    int dtype, mbit, scheme, l2_sc_bit, fused;
     bool operator==(const LutKey& o) const {
-        return dtype == o.dtype && mbit == o.mbit && scheme == o.scheme && l2_sc_bit == o.l2_sc_bit;
+        return dtype == o.dtype && mbit == o.mbit && scheme == o.scheme && l2_sc_bit == o.l2_sc_bit &&
+               fused == o.fused;
     }
 };
 
@@ -593,6 +596,7 @@ int hbq_fast_try(const void* x, void* y, void* l1, void* l2i, void* sch, void* c
     p.rem[0] = 1.0f / p.em[0];
     p.rem[1] = 1.0f / p.em[1];
     p.use_ceil = hp.sf.use_ceil;
+    p.fused = hp.fused;
     // the kernel quantizes the L1 scale to E5M3 without subnormals
     if (hp.sf.allow_sub || hp.sf.emax != 15.f || hp.sf.mshift != 8.f || hp.sf.emin != -14.f) return 0;
 
@@ -607,7 +611,7 @@ int hbq_fast_try(const void* x, void* y, void* l1, void* l2i, void* sch, void* c
                 return 0;
             g_cus[dev] = cus;
         }
-        const LutKey key{dtype, mbit, scheme, l2_sc_bit};
+        const LutKey key{dtype, mbit, scheme, l2_sc_bit, hp.fused};
         for (int i = 0; i < kLutSlots; ++i)
             if (g_state[dev][i] != 0 && g_keys[dev][i] == key) slot = i;
         if (slot >= 0 && g_state[dev][slot] < 0) return 0;

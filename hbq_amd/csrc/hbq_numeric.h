@@ -172,19 +172,30 @@ __device__ __forceinline__ float e5m3_scale(float s, int use_ceil) {
 // subnormals.  The exponent is taken from the binade: where the reference's
 // floor(R_T(log2 u)) is one larger (u a few ulps below 2^(e+1)) both routes
 // yield the same value, which the exhaustive element tests confirm.
+//
+// Two mantissa roundings, as the reference has two forms of this function:
+//   fused = false: the eager op sequence; the Python scalar 0.5004 is rounded to
+//     T and so is the sum, k = floor(R_T(|m| + R_T(0.5004)));
+//   fused = true: the torch.compile'd function that GLOBAL_FP_QUANT_CACHE serves
+//     (src/quantizer.py:38-63, HBQQuantizer's default use_quant_kernel=True): the
+//     fused kernel computes in fp32, k = floor(f32(|m| + f32(0.5004))).
+// |m| is exact in fp32 on both routes.  For fp32 tensors the two coincide.
 template <class T, int M>
-__device__ __forceinline__ float elem_quant(float u, uint32_t& code) {
+__device__ __forceinline__ float elem_quant(float u, uint32_t& code, bool fused = false) {
     constexpr float kShift = (float)(1 << M);
     constexpr float kInvShift = 1.0f / (float)(1 << M);
     constexpr float kMmax = (float)((1 << M) - 1);
     constexpr float kThr = 1.0f - 0.5f / (float)(1 << M);   // min_norm - 2^-(m+1)
     // T(0.5004): the scalar is rounded to T before the add
-    const float rnd = (T::dt == kF16) ? 0.50048828125f : (T::dt == kBF16 ? 0.5f : 0.5004f);
+    const float rnd_eager = (T::dt == kF16) ? 0.50048828125f : (T::dt == kBF16 ? 0.5f : 0.5004f);
+    const bool f32_sum = fused || T::dt == kF32;
+    const float rnd = f32_sum ? 0.5004f : rnd_eager;
     float a = fabsf(u);
     uint32_t sbit = (f2bits(u) >> 31) << (M + 2);
     float q;
     if (a < kThr) {
-        float k = floorf(T::round(a * kShift + rnd));
+        const float sum = a * kShift + rnd;   // a * 2^M is exact: one fp32 rounding
+        float k = floorf(f32_sum ? sum : T::round(sum));
         if (k > kMmax) k = 0.f;   // rounds up into the normal range: the reference zeroes it
         q = (u == 0.f) ? 0.f : copysignf(k * kInvShift, u);
         code = (u == 0.f) ? 0u : (sbit | (uint32_t)k);
@@ -194,7 +205,8 @@ __device__ __forceinline__ float elem_quant(float u, uint32_t& code) {
     } else {
         int e = a >= 4.0f ? 2 : binade(a);     // also covers +inf (saturates below)
         float m = (a * pow2f(-e) - 1.0f) * kShift;
-        float k = floorf(T::round(m + rnd));
+        const float sum = m + rnd;
+        float k = floorf(f32_sum ? sum : T::round(sum));
         if (k > kMmax) {
             if (e < 2) { k = 0.f; e += 1; } else { k = kMmax; }
         }

@@ -28,7 +28,7 @@
 
 namespace hbq {
 
-constexpr int kMxSlots = 8;
+constexpr int kMxSlots = 12;   // mbit + 6 * fused
 constexpr int kMxMaxWords = 10 * 1024 + 2;   // E2M5: binades 2^-7 .. 2^3, plus 2 sentinels
 constexpr int kMxMagBytes = 256;             // fp16 magnitudes of up to 128 levels
 constexpr int kMxTabBytes = (kMxMagBytes + kMxMaxWords + 15) / 16 * 16;
@@ -47,14 +47,14 @@ __device__ __forceinline__ float mx_level_value(int c) {
 }
 
 template <int M>
-__device__ __forceinline__ uint32_t mx_level(float u, float& mag) {
+__device__ __forceinline__ uint32_t mx_level(float u, float& mag, bool fused) {
     uint32_t c;
-    mag = fabsf(elem_quant<F16, M>(u, c));
+    mag = fabsf(elem_quant<F16, M>(u, c, fused));
     return c & ((1u << (M + 2)) - 1u);
 }
 
 template <int M>
-__global__ void build_mx_lut_kernel(int slot, int n, uint32_t lo_bits) {
+__global__ void build_mx_lut_kernel(int slot, int n, uint32_t lo_bits, int fused) {
     const int per = n + 2;
     uint8_t* tab = g_mx_tab[slot];
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < per; i += gridDim.x * blockDim.x) {
@@ -62,7 +62,7 @@ __global__ void build_mx_lut_kernel(int slot, int n, uint32_t lo_bits) {
         if (i == 0) u = 0.f;
         else if (i == per - 1) u = 65504.f;   // fp16 max: saturated
         else u = F16::load((uint16_t)(lo_bits + (uint32_t)(i - 1)));
-        const uint32_t lv = mx_level<M>(u, mag);
+        const uint32_t lv = mx_level<M>(u, mag, fused);
         tab[kMxMagBytes + i] = (uint8_t)lv;
         // the table stores one magnitude per level: every u of a level must give it
         if (F16::store(mag) != F16::store(mx_level_value<M>((int)lv))) atomicMax(&g_mx_bad[slot], 4);
@@ -74,9 +74,9 @@ __global__ void build_mx_lut_kernel(int slot, int n, uint32_t lo_bits) {
         // first value above the range) is already saturated
         int status = 0;
         float m0, m1, m2;
-        if (mx_level<M>(F16::load((uint16_t)(lo_bits - 1u)), m0) != 0u) status = 1;
-        if (mx_level<M>(F16::load((uint16_t)(lo_bits + (uint32_t)n)), m1) != (1u << (M + 2)) - 1u) status = 2;
-        if (mx_level<M>(65504.f, m2) != (1u << (M + 2)) - 1u || m1 != m2) status = 3;
+        if (mx_level<M>(F16::load((uint16_t)(lo_bits - 1u)), m0, fused) != 0u) status = 1;
+        if (mx_level<M>(F16::load((uint16_t)(lo_bits + (uint32_t)n)), m1, fused) != (1u << (M + 2)) - 1u) status = 2;
+        if (mx_level<M>(65504.f, m2, fused) != (1u << (M + 2)) - 1u || m1 != m2) status = 3;
         g_mx_status[slot] = status;
     }
 }
@@ -154,7 +154,7 @@ __global__ __launch_bounds__(kThreads) void mx_fast_kernel(const uint16_t* __res
             for (int i = 0; i < kV; ++i) {
                 const float v = F16::load((uint16_t)(i & 1 ? w[i / 2] >> 16 : w[i / 2] & 0xffffu));
                 const float yv = p.pot ? F16::round(v * rs) : div_T<F16>(v, s, rs);
-                const float q = elem_quant<F16, M>(yv, cout[i]);
+                const float q = elem_quant<F16, M>(yv, cout[i], p.fused);
                 out[i] = F16::round(q * s);
             }
 #pragma unroll
@@ -244,8 +244,8 @@ int g_mx_mbit[kMaxDevices][kMxSlots];   // element mantissa bits of the slot's t
 int g_mx_cus[kMaxDevices];
 
 template <int M>
-int build_mx_slot(int slot, int n, uint32_t lo_bits, hipStream_t st) {
-    hipLaunchKernelGGL((build_mx_lut_kernel<M>), dim3(32), dim3(256), 0, st, slot, n, lo_bits);
+int build_mx_slot(int slot, int n, uint32_t lo_bits, int fused, hipStream_t st) {
+    hipLaunchKernelGGL((build_mx_lut_kernel<M>), dim3(32), dim3(256), 0, st, slot, n, lo_bits, fused);
     hipError_t e = hipGetLastError();
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     if (e != hipSuccess) return -hbq_fail(HBQ_ERR_HIP, "MX level table build failed: %s", hipGetErrorString(e));
@@ -301,7 +301,7 @@ int hbq_mx_fast_try(const void* x, void* y, void* scales, void* codes, int64_t r
 
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
-    const int slot = mbit;   // one table per element format
+    const int slot = mbit + 6 * (p.fused != 0);   // one table per element format and rounding
     {
         std::lock_guard<std::mutex> g(g_mx_mu);
         if (g_mx_cus[dev] == 0) {
@@ -312,10 +312,11 @@ int hbq_mx_fast_try(const void* x, void* y, void* scales, void* codes, int64_t r
         }
         if (g_mx_mbit[dev][slot] < 0) return 0;
         if (g_mx_mbit[dev][slot] == 0) {
-            const int rc = mbit == 1 ? build_mx_slot<1>(slot, n, lo_bits, st)
-                           : mbit == 2 ? build_mx_slot<2>(slot, n, lo_bits, st)
-                           : mbit == 3 ? build_mx_slot<3>(slot, n, lo_bits, st)
-                                       : build_mx_slot<5>(slot, n, lo_bits, st);
+            const int fz = p.fused != 0;
+            const int rc = mbit == 1 ? build_mx_slot<1>(slot, n, lo_bits, fz, st)
+                           : mbit == 2 ? build_mx_slot<2>(slot, n, lo_bits, fz, st)
+                           : mbit == 3 ? build_mx_slot<3>(slot, n, lo_bits, fz, st)
+                                       : build_mx_slot<5>(slot, n, lo_bits, fz, st);
             if (rc < 0) return rc;
             g_mx_mbit[dev][slot] = rc == 0 ? mbit : -1;
             if (rc != 0) return 0;

@@ -49,7 +49,7 @@ __global__ __launch_bounds__(kThreads) void mxfp_qdq_kernel(const typename T::st
     for (int i = 0; i < kV; ++i) {
         // a power-of-two scale divides exactly: rounding x * 2^-e is R_T(x / s)
         float yv = p.pot ? T::round(v[i] * rs) : div_T<T>(v[i], s, rs);
-        float q = elem_quant<T, M>(yv, c[i]);
+        float q = elem_quant<T, M>(yv, c[i], p.fused);
         float o = T::round(q * s);
         if (p.per_tensor) o = T::round(o * p.tscale);
         v[i] = o;
@@ -119,11 +119,11 @@ __global__ __launch_bounds__(kThreads) void scale_quant_kernel(const typename T:
 template <class T, int M>
 __global__ __launch_bounds__(kThreads) void elem_quant_kernel(const typename T::storage* __restrict__ x,
                                                               typename T::storage* __restrict__ y,
-                                                              uint8_t* __restrict__ codes, int64_t n) {
+                                                              uint8_t* __restrict__ codes, int64_t n, int fused) {
     int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (i >= n) return;
     uint32_t c;
-    float q = elem_quant<T, M>(T::load(x[i]), c);
+    float q = elem_quant<T, M>(T::load(x[i]), c, fused);
     y[i] = T::store(q);
     if (codes) codes[i] = (uint8_t)c;
 }
@@ -502,7 +502,8 @@ int hbq_set_generic_only(int on) {
 
 int hbq_mxfp_qdq(const void* x, void* y, void* scales, void* codes, int64_t rows, int64_t cols, int dtype,
                  int block_size, int ebit, int mbit, int sc_ebit, int sc_mbit, int scale_allow_subnormal,
-                 int use_round, int use_ceil, int per_tensor_scale, double tensor_scale, void* stream) {
+                 int use_round, int use_ceil, int per_tensor_scale, double tensor_scale, int compiled,
+                 void* stream) {
     hbq_clear_error();
     if (dtype != kF16 && dtype != kBF16 && dtype != kF32) return hbq_fail(HBQ_ERR_INVALID, "bad dtype code %d", dtype);
     if (ebit != 2) return hbq_fail(HBQ_ERR_UNSUPPORTED, "element exponent bits %d not supported on the GPU path", ebit);
@@ -526,6 +527,7 @@ int hbq_mxfp_qdq(const void* x, void* y, void* scales, void* codes, int64_t rows
     }
     p.per_tensor = per_tensor_scale;
     p.tscale = round_host(tensor_scale, dtype);
+    p.fused = compiled != 0;
     hipStream_t st = (hipStream_t)stream;
     if (!g_hbq_force_generic) {
         const int fr = hbq_mx_fast_try(x, y, scales, codes, rows, cols, dtype, block_size, mbit, p, st);
@@ -569,7 +571,7 @@ static int hbq_setup(HbqParams& p, int& S, Geometry& g, const void* x, const voi
 int hbq_hbq_qdq(const void* x, void* y, void* l1_scale, void* l2_index, void* scheme, void* codes, int64_t rows,
                 int64_t cols, int dtype, int block_size, int ebit, int mbit, int sc_ebit, int sc_mbit,
                 int l2_block_size, int l2_sc_bit, int l2_scheme, int scale_allow_subnormal, int use_ceil,
-                void* stream) {
+                int compiled, void* stream) {
     hbq_clear_error();
     HbqParams p{};
     int S = 1;
@@ -577,6 +579,7 @@ int hbq_hbq_qdq(const void* x, void* y, void* l1_scale, void* l2_index, void* sc
     if (int rc = hbq_setup(p, S, g, x, y, codes, rows, cols, dtype, block_size, ebit, mbit, sc_ebit, sc_mbit,
                            l2_block_size, l2_sc_bit, l2_scheme, scale_allow_subnormal, use_ceil))
         return rc;
+    p.fused = compiled != 0;
     if (g.nb == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
     if (!g_hbq_force_generic) {
@@ -595,7 +598,7 @@ int hbq_hbq_qdq(const void* x, void* y, void* l1_scale, void* l2_index, void* sc
 
 int hbq_hbq_qdq_causal(void* x, int64_t mats, int64_t t, int dtype, int block_size, int ebit, int mbit, int sc_ebit,
                        int sc_mbit, int l2_block_size, int l2_sc_bit, int l2_scheme, int scale_allow_subnormal,
-                       int use_ceil, void* stream) {
+                       int use_ceil, int compiled, void* stream) {
     hbq_clear_error();
     if (mats < 0 || t < 0) return hbq_fail(HBQ_ERR_INVALID, "negative size");
     if (t % 128 || block_size != 128)
@@ -607,6 +610,7 @@ int hbq_hbq_qdq_causal(void* x, int64_t mats, int64_t t, int dtype, int block_si
     if (int rc = hbq_setup(p, S, g, x, x, nullptr, mats * t, t, dtype, block_size, ebit, mbit, sc_ebit, sc_mbit,
                            l2_block_size, l2_sc_bit, l2_scheme, scale_allow_subnormal, use_ceil))
         return rc;
+    p.fused = compiled != 0;
     if (g.nb == 0) return 0;
     const int fr = g_hbq_force_generic ? 0
                                        : hbq_fast_try(x, x, nullptr, nullptr, nullptr, nullptr, mats * t, t, dtype,
@@ -644,7 +648,8 @@ int hbq_scale_quant(const void* x, void* y, int64_t n, int dtype, int ebit, int 
     return hbq_check_launch("hbq_scale_quant");
 }
 
-int hbq_elem_quant(const void* x, void* y, void* codes, int64_t n, int dtype, int ebit, int mbit, void* stream) {
+int hbq_elem_quant(const void* x, void* y, void* codes, int64_t n, int dtype, int ebit, int mbit, int compiled,
+                   void* stream) {
     hbq_clear_error();
     if (ebit != 2) return hbq_fail(HBQ_ERR_UNSUPPORTED, "element exponent bits %d not supported on the GPU path", ebit);
     if (n < 0 || x == nullptr || y == nullptr) return hbq_fail(HBQ_ERR_INVALID, "bad arguments");
@@ -654,7 +659,7 @@ int hbq_elem_quant(const void* x, void* y, void* codes, int64_t n, int dtype, in
     hipStream_t st = (hipStream_t)stream;
 #define ELEM_CASE(TT, MB)                                                                                          \
     hipLaunchKernelGGL((elem_quant_kernel<TT, MB>), dim3((unsigned)grid), dim3(kThreads), 0, st,                   \
-                       (const TT::storage*)x, (TT::storage*)y, (uint8_t*)codes, n)
+                       (const TT::storage*)x, (TT::storage*)y, (uint8_t*)codes, n, compiled != 0)
 #define ELEM_M(TT)                                                                                                 \
     switch (mbit) {                                                                                                \
         case 1: ELEM_CASE(TT, 1); break;                                                                           \

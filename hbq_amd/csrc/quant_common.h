@@ -187,6 +187,7 @@ struct MxParams {
     ScaleFmt sf;          // FP scale format
     int per_tensor;
     float tscale;         // per-tensor scale, already rounded to T
+    int fused;            // element rounding of the compiled lpfp_quant (activate_dynamo=True)
 };
 
 template <class T, class Tab = ConstLog2>
@@ -211,6 +212,7 @@ struct HbqParams {
     float rl2[kMaxJ][2];         // correctly rounded reciprocals
     float em[2];                 // R_T(ele_max * max_j l2[j, s])
     ScaleFmt sf;                 // E5M3 L1 scale format
+    int fused;                   // element rounding of the compiled lpfp_quant (use_quant_kernel=True)
 };
 
 // Host: the L2 candidate factors of a scheme (HBQ_L2_* code) rounded to the

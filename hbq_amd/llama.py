@@ -135,7 +135,7 @@ def quantize_causal_(qz, p):
         rc = _lib.lib().hbq_hbq_qdq_causal(
             _lib.ptr(p), p.numel() // (T * T), T, _lib.DTYPE_CODE[p.dtype], qz.block_size, qz.ebit, qz.mbit,
             qz.sc_ebit, qz.sc_mbit, qz.l2_block_size, qz.l2_sc_bit, qz.L2_SCHEME.index(qz.l2_scheme),
-            int(qz.scale_allow_subnormal), int(qz.use_ceil), _lib.stream_of(p))
+            int(qz.scale_allow_subnormal), int(qz.use_ceil), int(qz._fused), _lib.stream_of(p))
         if rc == 0:
             return p
         if rc != _lib.ERR_UNSUPPORTED:

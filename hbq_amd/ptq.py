@@ -127,7 +127,8 @@ class PTQ:
                                 l2_block_size=self.act_l2_block_size if a else self.wgt_l2_block_size,
                                 l2_sc_bit=self.act_l2_sc_bit if a else self.wgt_l2_sc_bit,
                                 l2_scheme=self.act_l2_scheme if a else self.wgt_l2_scheme,
-                                use_quant_kernel=not self.large_model_memory_mode)
+                                # map_4b_kv_quantizer leaves the constructor default (src/ptq.py:242-253)
+                                use_quant_kernel=True if kv else not self.large_model_memory_mode)
         if qtype == "none":
             return _QBase()
         what = "weight" if side == "wgt" else "activation"

@@ -123,7 +123,12 @@ def _as_rows(x):
 
 def make_fp_quant(ebit: int, mbit: int, allow_subnormal: bool = True, detailed_output: bool = False,
                   use_ceil: bool = False, emax: int = None, emin: int = None):
-    """Element quantizer of E(ebit)M(mbit) (src/quantizer.py:187-257) as a GPU callable."""
+    """Element quantizer of E(ebit)M(mbit) (src/quantizer.py:187-257) as a GPU callable,
+    with the rounding of the eager op chain (each step rounded to the tensor dtype)."""
+    return _elem_quantizer(ebit, mbit, allow_subnormal, detailed_output, use_ceil, emax, emin, compiled=False)
+
+
+def _elem_quantizer(ebit, mbit, allow_subnormal, detailed_output, use_ceil, emax, emin, compiled):
     if ebit != 2 or not allow_subnormal or detailed_output or use_ceil or emax is not None or emin is not None:
         raise NotImplementedError(
             "the GPU element quantizer implements E2Mm with subnormals and nearest rounding only")
@@ -135,9 +140,10 @@ def make_fp_quant(ebit: int, mbit: int, allow_subnormal: bool = True, detailed_o
         xc = x.contiguous()
         y = torch.empty_like(xc)
         _lib.check(_lib.lib().hbq_elem_quant(_lib.ptr(xc), _lib.ptr(y), None, xc.numel(), _lib.DTYPE_CODE[x.dtype],
-                                             ebit, mbit, _lib.stream_of(xc)), NotImplementedError)
+                                             ebit, mbit, int(compiled), _lib.stream_of(xc)), NotImplementedError)
         return y
 
+    lpfp_quant.compiled = compiled
     return lpfp_quant
 
 
@@ -160,8 +166,11 @@ class FPQuantConfig:
 class FPQuantCompilerCache:
     """Cache of element quantizers by format (src/quantizer.py:38-65).
 
-    The reference compiles the eager op chain with torch.compile; here every
-    entry is the fused HIP kernel, so there is nothing to compile or warm up."""
+    The reference serves make_fp_quant's function compiled with torch.compile,
+    which fuses the op chain into one fp32 kernel: the sum |m| + 0.5004 is not
+    rounded to the tensor dtype, unlike the eager chain.  Every entry here is the
+    HIP element kernel with that fused rounding, so there is nothing to compile
+    or warm up."""
 
     def __init__(self):
         self._cache: Dict[tuple, Callable[[torch.Tensor], torch.Tensor]] = {}
@@ -169,8 +178,8 @@ class FPQuantCompilerCache:
     def get(self, cfg: FPQuantConfig) -> Callable[[torch.Tensor], torch.Tensor]:
         fn = self._cache.get(cfg.key)
         if fn is None:
-            fn = make_fp_quant(cfg.ebit, cfg.mbit, cfg.allow_subnormal, cfg.detailed_output, cfg.use_ceil,
-                               cfg.emax, cfg.emin)
+            fn = _elem_quantizer(cfg.ebit, cfg.mbit, cfg.allow_subnormal, cfg.detailed_output, cfg.use_ceil,
+                                 cfg.emax, cfg.emin, compiled=True)
             self._cache[cfg.key] = fn
         return fn
 
@@ -254,11 +263,16 @@ class MXFPQuantizer(_QBase):
         self.use_ceil = use_ceil
         lp_config = FPQuantConfig(ebit=self.ebit, mbit=self.mbit, allow_subnormal=True, detailed_output=False)
         self._lp_config = lp_config
-        self._activate_dynamo = activate_dynamo
+        # the element rounding follows the flag as in the reference (src/quantizer.py:464-469):
+        # the compiled function of GLOBAL_FP_QUANT_CACHE, or the eager make_fp_quant
+        self._fused = bool(activate_dynamo)
 
     @property
     def lpfp_quant(self):
-        return GLOBAL_FP_QUANT_CACHE.get(self._lp_config)
+        if self._fused:
+            return GLOBAL_FP_QUANT_CACHE.get(self._lp_config)
+        c = self._lp_config
+        return make_fp_quant(c.ebit, c.mbit, c.allow_subnormal, c.detailed_output, c.use_ceil, c.emax, c.emin)
 
     def reshape(self, x: torch.Tensor):
         return _reshape_to_blocks(x, [-1], block_size=self.block_size)
@@ -290,7 +304,7 @@ class MXFPQuantizer(_QBase):
             _lib.check(_lib.lib().hbq_mxfp_qdq(
                 _lib.ptr(xc), _lib.ptr(y), _lib.ptr(scales), _lib.ptr(codes), rows, cols, _lib.DTYPE_CODE[x.dtype],
                 block_size, self.ebit, self.mbit, self.sc_ebit, self.sc_mbit, int(self.scale_allow_subnormal),
-                int(self.use_round), int(self.use_ceil), int(per), float(ts), _lib.stream_of(xc)),
+                int(self.use_round), int(self.use_ceil), int(per), float(ts), int(self._fused), _lib.stream_of(xc)),
                 NotImplementedError)
         return y.view(x.shape), codes, scales
 
@@ -374,7 +388,7 @@ class HBQQuantizer(MXFPQuantizer):
                 _lib.ptr(xc), _lib.ptr(y), _lib.ptr(l1), _lib.ptr(l2i), _lib.ptr(sch), _lib.ptr(codes), rows, cols,
                 _lib.DTYPE_CODE[x.dtype], B, self.ebit, self.mbit, self.sc_ebit, self.sc_mbit, self.l2_block_size,
                 self.l2_sc_bit, self.L2_SCHEME.index(self.l2_scheme), int(self.scale_allow_subnormal),
-                int(self.use_ceil), _lib.stream_of(xc)), NotImplementedError)
+                int(self.use_ceil), int(self._fused), _lib.stream_of(xc)), NotImplementedError)
         return y.view(x.shape), codes, l1, l2i, sch
 
     def q(self, x: torch.Tensor):

@@ -14,6 +14,16 @@
  * with cols its last dimension; a ragged last block is zero padded, as
  * _reshape_to_blocks does (src/quantizer.py:67-146).
  *
+ * Element rounding (`compiled` argument of the quantizer entry points).  The
+ * reference's element quantizer exists in two forms that round differently:
+ * make_fp_quant's eager op chain (compiled = 0: the Python scalar 0.5004 and the
+ * sum |m| + 0.5004 are rounded to T) and the torch.compile'd function that
+ * GLOBAL_FP_QUANT_CACHE serves (compiled = 1: one fused fp32 kernel, the sum is
+ * not rounded to T), src/quantizer.py:38-63,202-255.  HBQQuantizer selects the
+ * compiled form with use_quant_kernel=True (its default, and what PTQ builds),
+ * MXFPQuantizer with activate_dynamo=True (src/quantizer.py:464-469,724).  The two
+ * differ on a few 16-bit inputs per element format; for fp32 tensors they agree.
+ *
  * Element codes (optional output, NULL to skip): sign | 2-bit exponent field
  * | m mantissa bits, exponent field 0 for subnormals, i.e. the OCP encodings
  * of E2M1/E2M2/E2M3/E2M5.  E2M1 codes are packed two per byte (even column
@@ -50,7 +60,7 @@ extern "C" {
 /* Message of the last failing call on this thread ("" after a success). */
 const char *hbq_last_error(void);
 
-/* ABI revision of this header. */
+/* ABI revision of this header (2: the `compiled` element-rounding argument). */
 int hbq_abi_version(void);
 
 /* No reference counterpart: a test hook.  on != 0 routes every hbq_hbq_qdq and
@@ -71,7 +81,8 @@ int hbq_set_generic_only(int on);
  */
 int hbq_mxfp_qdq(const void *x, void *y, void *scales, void *codes, int64_t rows, int64_t cols, int dtype,
                  int block_size, int ebit, int mbit, int sc_ebit, int sc_mbit, int scale_allow_subnormal,
-                 int use_round, int use_ceil, int per_tensor_scale, double tensor_scale, void *stream);
+                 int use_round, int use_ceil, int per_tensor_scale, double tensor_scale, int compiled,
+                 void *stream);
 
 /*
  * HBQ two-level quantize-dequantize.
@@ -87,7 +98,7 @@ int hbq_mxfp_qdq(const void *x, void *y, void *scales, void *codes, int64_t rows
 int hbq_hbq_qdq(const void *x, void *y, void *l1_scale, void *l2_index, void *scheme, void *codes, int64_t rows,
                 int64_t cols, int dtype, int block_size, int ebit, int mbit, int sc_ebit, int sc_mbit,
                 int l2_block_size, int l2_sc_bit, int l2_scheme, int scale_allow_subnormal, int use_ceil,
-                void *stream);
+                int compiled, void *stream);
 
 /* The attention-weight quantizer of the causal manual attention (src/module.py:113-116,
  * HBQQuantizer.q on the softmax output) in place on x [mats, t, t] (fp16 / bf16,
@@ -98,7 +109,7 @@ int hbq_hbq_qdq(const void *x, void *y, void *l1_scale, void *l2_index, void *sc
  * then uses hbq_hbq_qdq). */
 int hbq_hbq_qdq_causal(void *x, int64_t mats, int64_t t, int dtype, int block_size, int ebit, int mbit, int sc_ebit,
                        int sc_mbit, int l2_block_size, int l2_sc_bit, int l2_scheme, int scale_allow_subnormal,
-                       int use_ceil, void *stream);
+                       int use_ceil, int compiled, void *stream);
 
 /*
  * Packed HBQ tensors (no reference counterpart in src/: the bit layout of the
@@ -151,10 +162,12 @@ int hbq_gemm_packed_w(const void *A, const void *pcodes, const void *pl1, const 
 
 /*
  * Elementwise E2Mm quantization with subnormals.
- * Replaces the callable returned by make_fp_quant(ebit, mbit) (src/quantizer.py:187-257)
- * and served by GLOBAL_FP_QUANT_CACHE (src/quantizer.py:38-65).  codes optional, one byte each.
+ * Replaces the callable returned by make_fp_quant(ebit, mbit) (src/quantizer.py:187-257,
+ * compiled = 0) and the compiled one GLOBAL_FP_QUANT_CACHE serves (src/quantizer.py:38-65,
+ * compiled = 1).  codes optional, one byte each.
  */
-int hbq_elem_quant(const void *x, void *y, void *codes, int64_t n, int dtype, int ebit, int mbit, void *stream);
+int hbq_elem_quant(const void *x, void *y, void *codes, int64_t n, int dtype, int ebit, int mbit, int compiled,
+                   void *stream);
 
 /*
  * Elementwise scale quantization to E(ebit)M(mbit), half-up (use_ceil=0) or

@@ -17,6 +17,7 @@
  * Reference files (SeoLabCornell/HBQ):
  *   src/quantizer.py:148-185  format constants            -> max_norm/min_norm/min_subnorm
  *   src/quantizer.py:187-257  make_fp_quant (elements)     -> fpq_value(..., rnd=0.5004f)
+ *   src/quantizer.py:38-63    its torch.compile'd form     -> fpq_value_fused
  *   src/quantizer.py:259-328  fp_quant (scales)            -> fpq_value(..., rnd=0.5f)
  *   src/quantizer.py:481-511  MXFPQuantizer.get_shared_scale -> mx_pot_scale / nv_fp_scale
  *   src/quantizer.py:513-539  MXFPQuantizer.q              -> orc_mxfp_qdq
@@ -178,6 +179,55 @@ static float fpq_value(float x, const fmt_t *f, int dt, float rnd, int allow_sub
     return xq;
 }
 
+/*
+ * make_fp_quant's callable as GLOBAL_FP_QUANT_CACHE serves it
+ * (src/quantizer.py:38-63): torch.compile(fullgraph=True) fuses the whole
+ * function (src/quantizer.py:202-255) into one kernel that loads the T value,
+ * computes every step in fp32 and rounds to T only at the store.  The comment
+ * at src/quantizer.py:224-228 describes exactly this difference from the eager
+ * op sequence.  So here, unlike fpq_value:
+ *   - floor(log2|x|) is taken in fp32: the exact floor for a 16-bit value (its
+ *     fp32 log2 lies at least 2^-12 below the next integer, far above the fp32
+ *     spacing there), taken from the binade;
+ *   - the mantissa rounding is floor(f32(|m| + f32(0.5004))), with the fp32
+ *     constant 0x3F001A37 and no rounding of the sum to T;
+ *   - the .to(x.dtype) of that sum is a cast of an fp16-typed value to its own
+ *     dtype, which the compiled graph drops.
+ * |m| itself is exact in fp32 on both routes.  For fp32 tensors the eager op
+ * sequence is already all fp32, so both routes coincide and fp32 uses fpq_value.
+ * Pinned by tests/golden/compiled_quant.npz (exhaustive over all 16-bit inputs).
+ */
+static float fpq_value_fused(float x, const fmt_t *f, int dt) {
+    if (dt == DT_F32) return fpq_value(x, f, dt, 0.5004f, 1, 0);
+    float a = fabsf(x);
+    int is_zero = (x == 0.f);
+    int promote = (a < f->min_norm) && (a >= f->thr);
+    int sub = (a < f->thr) && !is_zero;
+    float fe;
+    if (is_zero) fe = 0.f;                       /* log2(|0| + 1) */
+    else if (a != a || a == INFINITY) fe = a;    /* log2 of NaN / inf */
+    else { int ex; frexpf(a, &ex); fe = (float)(ex - 1); }
+    float e = fe < f->emin ? f->emin : (fe > f->emax ? f->emax : fe);   /* clip keeps NaN */
+    float p2 = exp2f(e);
+    float sg = sign_of(x);
+    float mant = sub ? (x / p2) * f->mshift : (x / p2 - sg) * f->mshift;
+    volatile float sum = fabsf(mant) + 0.5004f;   /* one fp32 rounding, no contraction */
+    float mr = floorf(sum);
+    int overflow = (mr > f->mmax) && (e != f->emax);
+    if (mr > f->mmax) mr = f->mmax;
+    if (is_zero || overflow || promote) mr = 0.f;
+    if (overflow) e = e + 1.f;
+    float smant = sg * mr;
+    float p2b = exp2f(e);
+    float xq = sub ? (smant / f->mshift) * p2b : (smant / f->mshift + sg) * p2b;
+    if (is_zero) xq = 0.f;
+    return rT(xq, dt);
+}
+
+static inline float elem_value(float x, const fmt_t *f, int dt, int compiled) {
+    return compiled ? fpq_value_fused(x, f, dt) : fpq_value(x, f, dt, 0.5004f, 1, 0);
+}
+
 /* MX power-of-two shared scale (src/quantizer.py:489-503) */
 static float mx_pot_scale(float amax, int dt, int ebit, int sc_ebit, int use_round) {
     float mn = (dt == DT_F32) ? 1.17549435e-38f : 6.103515625e-05f;
@@ -266,10 +316,13 @@ float orc_row_sum(const float *v, int64_t n) { return row_sum(v, n); }
 /* ------------------------------------------------------------------------- */
 /* exported scalar tables                                                     */
 /* ------------------------------------------------------------------------- */
-int orc_elem_quant(const void *x, void *y, int64_t n, int dt, int ebit, int mbit, int use_ceil) {
+int orc_elem_quant(const void *x, void *y, int64_t n, int dt, int ebit, int mbit, int use_ceil, int compiled) {
     fmt_t f;
     fmt_init(&f, ebit, mbit);
-    for (int64_t i = 0; i < n; ++i) st(y, i, dt, fpq_value(ld(x, i, dt), &f, dt, 0.5004f, 1, use_ceil));
+    if (compiled && use_ceil) return -1;   /* the cache only serves use_ceil=False */
+    for (int64_t i = 0; i < n; ++i)
+        st(y, i, dt, compiled ? fpq_value_fused(ld(x, i, dt), &f, dt)
+                              : fpq_value(ld(x, i, dt), &f, dt, 0.5004f, 1, use_ceil));
     return 0;
 }
 
@@ -302,7 +355,7 @@ int orc_mx_scale(const void *amax, void *y, int64_t n, int dt, int ebit, int mbi
 /* ------------------------------------------------------------------------- */
 int orc_mxfp_qdq(const void *x, void *y, void *scale_out, int64_t rows, int64_t cols, int dt,
                  int block, int ebit, int mbit, int sc_ebit, int sc_mbit, int allow_sub,
-                 int use_round, int use_ceil, int per_tensor, double tensor_scale) {
+                 int use_round, int use_ceil, int per_tensor, double tensor_scale, int compiled) {
     if (block <= 0 || block > 4096) return -1;
     int64_t nblk = (cols + block - 1) / block;
     fmt_t f;
@@ -326,7 +379,7 @@ int orc_mxfp_qdq(const void *x, void *y, void *scale_out, int64_t rows, int64_t 
                 int64_t c = b * block + i;
                 if (c >= cols) break;
                 float yv = rT(v[i] / s, dt);
-                float q = fpq_value(yv, &f, dt, 0.5004f, 1, 0);
+                float q = elem_value(yv, &f, dt, compiled);
                 float o = rT(q * s, dt);
                 if (per_tensor) o = rT(o * ts, dt);
                 st(y, r * cols + c, dt, o);
@@ -378,7 +431,8 @@ static inline int better(float v, float best) { return (v != v) ? (best == best)
 
 int orc_hbq_qdq(const void *x, void *y, void *l1_out, uint8_t *l2idx_out, uint8_t *scheme_out,
                 void *l2val_out, int64_t rows, int64_t cols, int dt, int block, int ebit, int mbit,
-                int sc_ebit, int sc_mbit, int l2b, int l2_sc_bit, int scheme, int allow_sub, int use_ceil) {
+                int sc_ebit, int sc_mbit, int l2b, int l2_sc_bit, int scheme, int allow_sub, int use_ceil,
+                int compiled) {
     if (block <= 0 || block > HBQ_MAXB || l2b <= 0 || block % l2b) return -1;
     if (l2_sc_bit < 0 || (1 << l2_sc_bit) > HBQ_MAXJ) return -1;
     float tab[HBQ_MAXJ * HBQ_MAXS];
@@ -421,7 +475,7 @@ int orc_hbq_qdq(const void *x, void *y, void *l1_out, uint8_t *l2idx_out, uint8_
                     for (int j = 0; j < J; ++j) {
                         float l2 = tab[j * S + s];
                         float u = rT(t / l2, dt);
-                        float q = fpq_value(u, &f, dt, 0.5004f, 1, 0);
+                        float q = elem_value(u, &f, dt, compiled);
                         float dq = rT(rT(q * l2, dt) * l1[s], dt);
                         float e = fabsf(rT(xv[i] - dq, dt));
                         d[(i * J + j) * S + s] = dq;

@@ -34,13 +34,13 @@ def lib():
         L = ctypes.CDLL(LIB_PATH)
         P, I, I64, D = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_double
         sig = {
-            "orc_elem_quant": [P, P, I64, I, I, I, I],
+            "orc_elem_quant": [P, P, I64, I, I, I, I, I],
             "orc_fp_quant": [P, P, I64, I, I, I, I, I],
             "orc_floor_log2": [P, P, I64, I],
             "orc_mx_scale": [P, P, I64, I, I, I, I, I, I, I, I],
-            "orc_mxfp_qdq": [P, P, P, I64, I64, I, I, I, I, I, I, I, I, I, I, D],
+            "orc_mxfp_qdq": [P, P, P, I64, I64, I, I, I, I, I, I, I, I, I, I, D, I],
             "orc_hbq_l2_table": [I, I, I, P],
-            "orc_hbq_qdq": [P, P, P, P, P, P, I64, I64, I, I, I, I, I, I, I, I, I, I, I],
+            "orc_hbq_qdq": [P, P, P, P, P, P, I64, I64, I, I, I, I, I, I, I, I, I, I, I, I],
             "orc_gemm_fp32acc": [P, P, P, I, I, I],
             "orc_gemm_fp16acc": [P, P, P, I, I, I],
             "orc_gemm_grouped": [P, P, P, I, I, I, I],
@@ -80,11 +80,16 @@ def _check(rc, name):
         raise RuntimeError(f"oracle {name} failed with code {rc}")
 
 
-def elem_quant(x, dt, ebit, mbit, use_ceil=False):
-    """make_fp_quant(ebit, mbit) elementwise (src/quantizer.py:187-257)."""
+def elem_quant(x, dt, ebit, mbit, use_ceil=False, compiled=False):
+    """make_fp_quant(ebit, mbit) elementwise (src/quantizer.py:187-257).
+
+    compiled=True gives the torch.compile'd form GLOBAL_FP_QUANT_CACHE serves
+    (src/quantizer.py:38-63): every step in fp32, the sum |m| + 0.5004 not
+    rounded to T."""
     x = _bits(x, dt)
     y = _empty(x.shape, dt)
-    _check(lib().orc_elem_quant(_p(x), _p(y), x.size, DT[dt], ebit, mbit, int(use_ceil)), "elem_quant")
+    _check(lib().orc_elem_quant(_p(x), _p(y), x.size, DT[dt], ebit, mbit, int(use_ceil), int(compiled)),
+           "elem_quant")
     return y
 
 
@@ -115,10 +120,11 @@ def mx_scale(amax, dt, ebit, mbit, sc_ebit, sc_mbit, allow_subnormal=False, use_
 
 
 def mxfp_qdq(x, dt, block_size, ebit, mbit, sc_ebit, sc_mbit, scale_allow_subnormal=False, use_round=False,
-             use_ceil=False, tensor_scale=None):
+             use_ceil=False, tensor_scale=None, compiled=False):
     """MXFPQuantizer.q (src/quantizer.py:513-539) on a 2-D array; blocks along the last dim.
 
-    Returns (dequantized, per-block scales)."""
+    compiled selects the element rule of activate_dynamo=True.  Returns
+    (dequantized, per-block scales)."""
     x = _bits(x, dt)
     rows, cols = x.shape
     nblk = -(-cols // block_size)
@@ -127,7 +133,7 @@ def mxfp_qdq(x, dt, block_size, ebit, mbit, sc_ebit, sc_mbit, scale_allow_subnor
     per = tensor_scale is not None
     _check(lib().orc_mxfp_qdq(_p(x), _p(y), _p(s), rows, cols, DT[dt], block_size, ebit, mbit, sc_ebit, sc_mbit,
                               int(scale_allow_subnormal), int(use_round), int(use_ceil), int(per),
-                              float(tensor_scale) if per else 1.0), "mxfp_qdq")
+                              float(tensor_scale) if per else 1.0, int(compiled)), "mxfp_qdq")
     return y, s
 
 
@@ -139,9 +145,12 @@ def l2_table(scheme, l2_sc_bit, dt):
 
 
 def hbq_qdq(x, dt, block_size=128, ebit=2, mbit=3, sc_ebit=5, sc_mbit=3, l2_block_size=4, l2_sc_bit=1,
-            l2_scheme="PoT", scale_allow_subnormal=False, use_ceil=False):
+            l2_scheme="PoT", scale_allow_subnormal=False, use_ceil=False, use_quant_kernel=True):
     """HBQQuantizer.q (src/quantizer.py:741-859) on a 2-D array.
 
+    use_quant_kernel selects the element rule as the reference's flag does, with
+    the same default: True is the torch.compile'd lpfp_quant
+    (src/quantizer.py:468-469,724), False the eager one.
     Returns dict(y, l1, l2idx, scheme, l2val) mirroring the keep_l2_scale
     attributes shared_scale, l2_scale, blk_l2_scheme, real_l2_scale."""
     x = _bits(x, dt)
@@ -155,7 +164,7 @@ def hbq_qdq(x, dt, block_size=128, ebit=2, mbit=3, sc_ebit=5, sc_mbit=3, l2_bloc
     l2v = _empty((rows, nblk, nsub), dt)
     _check(lib().orc_hbq_qdq(_p(x), _p(y), _p(l1), _p(l2i), _p(sch), _p(l2v), rows, cols, DT[dt], block_size, ebit,
                              mbit, sc_ebit, sc_mbit, l2_block_size, l2_sc_bit, SCHEMES.index(l2_scheme),
-                             int(scale_allow_subnormal), int(use_ceil)), "hbq_qdq")
+                             int(scale_allow_subnormal), int(use_ceil), int(use_quant_kernel)), "hbq_qdq")
     return {"y": y, "l1": l1, "l2idx": l2i, "scheme": sch, "l2val": l2v}
 
 

@@ -109,10 +109,11 @@ def bits_value(b, dt):
 
 # ---- codes of a reference quantization ------------------------------------------------------------
 
-def hbq_codes(x, dt, res, block_size, mbit, l2_block_size, l2_sc_bit, l2_scheme):
+def hbq_codes(x, dt, res, block_size, mbit, l2_block_size, l2_sc_bit, l2_scheme, use_quant_kernel=True):
     """Element codes of HBQQuantizer.q's selected candidate (src/quantizer.py:781-791):
     t = R(x / l1_s), u = R(t / l2[j][s]), q = lpfp(u); code = sign | level(|q|).
-    res is oracle.hbq_qdq's result for the same x; the sign is that of its output."""
+    res is oracle.hbq_qdq's result for the same x and the same use_quant_kernel (the
+    element rounding); the sign is that of its output."""
     x = O._bits(x, dt)
     rows, cols = x.shape
     tab = O.l2_table(l2_scheme, l2_sc_bit, dt).astype(np.float64)
@@ -124,7 +125,7 @@ def hbq_codes(x, dt, res, block_size, mbit, l2_block_size, l2_sc_bit, l2_scheme)
     xv = bits_value(x, dt)
     t = bits_value(round_bits(xv / l1, dt), dt)
     u = round_bits(t / tab[j, s], dt)
-    q = bits_value(O.elem_quant(u, dt, 2, mbit), dt)
+    q = bits_value(O.elem_quant(u, dt, 2, mbit, compiled=use_quant_kernel), dt)
     lev = level_of(np.abs(q), mbit)
     y = res["y"]
     neg = np.signbit(y) if dt == "f32" else (y.astype(np.int64) >> 15) & 1

@@ -43,3 +43,15 @@ def golden_mxfp():
 @pytest.fixture(scope="session")
 def golden_hbq():
     return np.load(os.path.join(GOLDEN, "hbq_quant.npz"))
+
+
+@pytest.fixture(scope="session")
+def golden_compiled():
+    """use_quant_kernel=True / activate_dynamo=True fixtures: the torch.compile'd element quantizer."""
+    return np.load(os.path.join(GOLDEN, "compiled_quant.npz"))
+
+
+@pytest.fixture(scope="session")
+def golden_extra():
+    """The MXFP per-tensor scale branch and PoT HBQ on the weight and bf16 inputs."""
+    return np.load(os.path.join(GOLDEN, "extra_quant.npz"))

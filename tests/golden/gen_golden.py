@@ -15,10 +15,22 @@ library routine pins are executed:
   depends on torch's fp32 accumulation order inside ``sum``: HBQ-A/HBQ-E
   activation and weight variants and the 4-bit KV variant, fp16 and bf16,
   with ``keep_l2_scale=True`` so the L1/L2/scheme choices are recorded.
+* The ``torch.compile``d element quantizer that ``GLOBAL_FP_QUANT_CACHE``
+  serves (``src/quantizer.py:38-63``) and that ``HBQQuantizer`` uses by default
+  (``use_quant_kernel=True``, ``src/quantizer.py:468-469,724``), which is what
+  ``PTQ`` builds for every HBQ quantizer: exhaustive element tables and the
+  HBQ fixtures again with ``use_quant_kernel=True`` (``compiled_quant.npz``).
+  Inductor compiles it for the CPU here (g++); the generator records whether
+  the compile fell back to eager (``src/quantizer.py:57-60``).
+* ``MXFPQuantizer.q`` with ``per_tensor_scale=True`` (``src/quantizer.py:516-524,
+  535-536``), and the PoT HBQ variant on the weight and bf16 inputs
+  (``extra_quant.npz``).
 
 Usage:  python tests/golden/gen_golden.py [/root/reference]
 """
+import contextlib
 import importlib.util
+import io
 import os
 import sys
 
@@ -148,7 +160,65 @@ def main():
                          use_quant_kernel=False, **hbcfgs["hbq_a_act"])
     hb["hbq_a_act_ragged_f16"] = u16(q.q(xr.clone()))
     np.savez_compressed(os.path.join(HERE, "hbq_quant.npz"), **hb)
+
+    write_compiled(ref, inputs, hbcfgs, mxcfgs, x16, x32)
+    write_extra(ref, inputs, hbcfgs, mxcfgs)
     print("wrote", sorted(os.listdir(HERE)))
+
+
+def write_compiled(ref, inputs, hbcfgs, mxcfgs, x16, x32):
+    """The compiled element quantizer, alone and inside HBQQuantizer.q / MXFPQuantizer.q."""
+    cq = {"torch_version": np.array(torch.__version__)}
+    allbits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
+    fell_back = False
+    for (e, m) in ((2, 1), (2, 2), (2, 5)):
+        cfg = ref.FPQuantConfig(ebit=e, mbit=m, allow_subnormal=True, detailed_output=False)
+        buf = io.StringIO()
+        with contextlib.redirect_stdout(buf):   # the cache prints a message when it falls back
+            f = ref.GLOBAL_FP_QUANT_CACHE.get(cfg)
+        fell_back |= "compile failed" in buf.getvalue()
+        for dt, dname in ((torch.float16, "f16"), (torch.bfloat16, "bf16")):
+            cq[f"elem_{dname}_e{e}m{m}"] = u16(f(allbits.view(dt).clone()))
+    cq["compile_fell_back"] = np.array(bool(fell_back))
+    for name, kw in hbcfgs.items():
+        for k, v in inputs.items():
+            q = ref.HBQQuantizer(block_size=128, sc_ebit=5, sc_mbit=3, keep_l2_scale=True,
+                                 scale_allow_subnormal=False, use_quant_kernel=True, **kw)
+            y = q.q(v.clone())
+            cq[f"{name}_{k}"] = u16(y)
+            cq[f"{name}_{k}_l1"] = u16(q.shared_scale)
+            cq[f"{name}_{k}_l2idx"] = q.l2_scale.numpy().astype(np.uint8)
+            cq[f"{name}_{k}_scheme"] = q.blk_l2_scheme.numpy().astype(np.uint8)
+    for name in ("mxfp4", "mxfp8", "nvfp4"):
+        q = ref.MXFPQuantizer(scale_allow_subnormal=False, activate_dynamo=True, **mxcfgs[name])
+        cq[f"{name}_f16"] = u16(q.q(x16.clone()))
+        cq[f"{name}_f32"] = q.q(x32.clone()).numpy()
+    np.savez_compressed(os.path.join(HERE, "compiled_quant.npz"), **cq)
+
+
+def write_extra(ref, inputs, hbcfgs, mxcfgs):
+    """Branches no configuration turns on: the NVFP per-tensor scale, PoT HBQ on more inputs."""
+    ex = {"torch_version": np.array(torch.__version__)}
+    xs16 = synth_rows(16, 512, 3001, torch.float16)
+    xs32 = synth_rows(16, 512, 3002, torch.float32)
+    ex["x_f16"] = u16(xs16)
+    ex["x_f32"] = xs32.numpy()
+    ex["x_zero_f16"] = u16(torch.zeros(4, 64, dtype=torch.float16))
+    for name in ("nvfp4", "mxfp4"):
+        q = ref.MXFPQuantizer(scale_allow_subnormal=False, per_tensor_scale=True, **mxcfgs[name])
+        ex[f"{name}_pts_f16"] = u16(q.q(xs16.clone()))
+        ex[f"{name}_pts_f32"] = q.q(xs32.clone()).numpy()
+        ex[f"{name}_pts_zero_f16"] = u16(q.q(torch.zeros(4, 64, dtype=torch.float16)))
+    for k in ("f16w", "bf16"):
+        q = ref.HBQQuantizer(block_size=128, sc_ebit=5, sc_mbit=3, keep_l2_scale=True,
+                             scale_allow_subnormal=False, use_quant_kernel=False, **hbcfgs["hbq_pot"])
+        y = q.q(inputs[k].clone())
+        ex[f"hbq_pot_{k}"] = u16(y)
+        ex[f"hbq_pot_{k}_l1"] = u16(q.shared_scale)
+        ex[f"hbq_pot_{k}_l2idx"] = q.l2_scale.numpy().astype(np.uint8)
+        ex[f"hbq_pot_{k}_scheme"] = q.blk_l2_scheme.numpy().astype(np.uint8)
+        ex[f"hbq_pot_{k}_l2val"] = u16(q.real_l2_scale)
+    np.savez_compressed(os.path.join(HERE, "extra_quant.npz"), **ex)
 
 
 if __name__ == "__main__":

@@ -43,7 +43,7 @@ def test_python_signatures_cover_header():
 
 def test_abi_version_and_error_string(lib):
     lib.hbq_abi_version.restype = ctypes.c_int
-    assert lib.hbq_abi_version() == 1
+    assert lib.hbq_abi_version() == 2
     lib.hbq_last_error.restype = ctypes.c_char_p
     assert lib.hbq_last_error() == b""
 
@@ -59,10 +59,10 @@ def test_argument_errors_without_gpu(lib):
     fake = ctypes.c_void_p(256)            # never dereferenced: the shape check fails first
     rc = L.hbq_gemm_blockquant_mxint8(fake, fake, fake, 4, 32, 100, 128, 32, 0, None)
     assert rc == 1 and L.hbq_last_error() == b"K must be divisible by group_k"
-    rc = L.hbq_hbq_qdq(None, None, None, None, None, None, 1, 128, 0, 128, 2, 2, 5, 3, 8, 2, 9, 0, 0, None)
+    rc = L.hbq_hbq_qdq(None, None, None, None, None, None, 1, 128, 0, 128, 2, 2, 5, 3, 8, 2, 9, 0, 0, 1, None)
     assert rc == 1
     rc = L.hbq_mxfp_qdq(ctypes.c_void_p(16), ctypes.c_void_p(16), None, None, 1, 96, 0, 48, 2, 1, 5, 0, 0, 0, 0,
-                        0, 1.0, None)
+                        0, 1.0, 1, None)
     assert rc == 2 and b"block_size" in L.hbq_last_error()
 
 
@@ -104,7 +104,7 @@ def test_decoder_kernel_argument_errors_without_gpu(lib):
     assert L.hbq_causal_softmax(fake, fake, 2, 128, 1.0, 2, None) == 2
     assert L.hbq_causal_softmax(None, None, 0, 128, 1.0, 0, None) == 0
     # causal quantizer: t % 128, block size, fp32, the quantizer's own checks (ebit)
-    args = (0, 128, 2, 2, 5, 3, 8, 2, 2, 0, 0, None)
+    args = (0, 128, 2, 2, 5, 3, 8, 2, 2, 0, 0, 1, None)
     assert L.hbq_hbq_qdq_causal(fake, 2, 192, *args) == 2
     assert L.hbq_hbq_qdq_causal(fake, 2, 256, 0, 64, *args[2:]) == 2
     assert L.hbq_hbq_qdq_causal(fake, 2, 256, 2, *args[1:]) == 2

@@ -40,14 +40,17 @@ def _hbq(kw, **extra):
 
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("em", [(2, 1), (2, 2), (2, 5)])
-def test_element_quantizer_exhaustive(gpu, golden_elem, dt, em):
-    """make_fp_quant over all 65,536 bit patterns equals the reference table."""
-    from hbq_amd.quantizer import make_fp_quant
+def test_element_quantizer_exhaustive(gpu, golden_elem, golden_compiled, dt, em):
+    """make_fp_quant (eager) and GLOBAL_FP_QUANT_CACHE's compiled quantizer over all 65,536
+    bit patterns equal the reference's tables (src/quantizer.py:38-63,187-257)."""
+    from hbq_amd.quantizer import FPQuantConfig, GLOBAL_FP_QUANT_CACHE, make_fp_quant
     print(f"elem dt={dt} E{em[0]}M{em[1]}", flush=True)
     allb = np.arange(65536, dtype=np.uint32).astype(np.uint16)
     x = to_torch(allb, dt).to(gpu)
-    y = make_fp_quant(*em)(x)
-    assert mismatches(to_bits(y), golden_elem[f"elem_{dt}_e{em[0]}m{em[1]}"], dt) == 0
+    key = f"elem_{dt}_e{em[0]}m{em[1]}"
+    assert mismatches(to_bits(make_fp_quant(*em)(x)), golden_elem[key], dt) == 0
+    fused = GLOBAL_FP_QUANT_CACHE.get(FPQuantConfig(ebit=em[0], mbit=em[1]))
+    assert mismatches(to_bits(fused(x)), golden_compiled[key], dt) == 0
 
 
 @pytest.mark.parametrize("dt", ["f16", "bf16", "f32"])
@@ -103,25 +106,50 @@ def test_mxfp_bf16_raises(gpu):
 
 @pytest.mark.parametrize("name", list(HBQCFG))
 @pytest.mark.parametrize("inp", ["f16", "f16w", "bf16"])
-def test_hbq_golden(gpu, golden_hbq, name, inp):
+@pytest.mark.parametrize("uqk", [False, True])
+def test_hbq_golden(gpu, golden_hbq, golden_extra, golden_compiled, name, inp, uqk):
+    """HBQQuantizer.q against the reference's outputs: use_quant_kernel=False (the eager element
+    quantizer) and True (the compiled one, the default PTQ builds)."""
     key = f"{name}_{inp}"
-    if key not in golden_hbq:
-        pytest.skip("no fixture")
-    print(f"hbq golden {key}", flush=True)
+    fx = golden_compiled if uqk else (golden_hbq if key in golden_hbq.files else golden_extra)
+    print(f"hbq golden {key} use_quant_kernel={uqk}", flush=True)
     dt = "bf16" if inp == "bf16" else "f16"
-    q = _hbq(HBQCFG[name], keep_l2_scale=True)
+    q = _hbq(HBQCFG[name], keep_l2_scale=True, use_quant_kernel=uqk)
     x = to_torch(golden_hbq[f"x_{inp}"], dt).to(gpu)
     y = q.q(x)
-    assert mismatches(to_bits(y), golden_hbq[key], dt) == 0
-    assert mismatches(to_bits(q.shared_scale), golden_hbq[key + "_l1"], dt) == 0
-    assert np.array_equal(q.l2_scale.cpu().numpy(), golden_hbq[key + "_l2idx"].astype(np.int64))
-    assert np.array_equal(q.blk_l2_scheme.cpu().numpy(), golden_hbq[key + "_scheme"].astype(np.int64))
-    assert mismatches(to_bits(q.real_l2_scale), golden_hbq[key + "_l2val"], dt) == 0
+    assert mismatches(to_bits(y), fx[key], dt) == 0
+    assert mismatches(to_bits(q.shared_scale), fx[key + "_l1"], dt) == 0
+    assert np.array_equal(q.l2_scale.cpu().numpy(), fx[key + "_l2idx"].astype(np.int64))
+    assert np.array_equal(q.blk_l2_scheme.cpu().numpy(), fx[key + "_scheme"].astype(np.int64))
+    if not uqk:
+        assert mismatches(to_bits(q.real_l2_scale), fx[key + "_l2val"], dt) == 0
+
+
+@pytest.mark.parametrize("name", ["mxfp4", "mxfp8", "nvfp4"])
+def test_mxfp_compiled_golden(gpu, golden_mxfp, golden_compiled, name):
+    """MXFPQuantizer(activate_dynamo=True): the compiled element quantizer inside MXFP q."""
+    q = _mx(MXCFG[name], activate_dynamo=True)
+    x = to_torch(golden_mxfp["x_f16"], "f16").to(gpu)
+    assert mismatches(to_bits(q.q(x)), golden_compiled[f"{name}_f16"], "f16") == 0
+    x32 = torch.from_numpy(golden_mxfp["x_f32"]).to(gpu)
+    assert mismatches(to_bits(q.q(x32)), golden_compiled[f"{name}_f32"], "f32") == 0
+
+
+@pytest.mark.parametrize("name", ["nvfp4", "mxfp4"])
+def test_mxfp_per_tensor_scale_golden(gpu, golden_extra, name):
+    """per_tensor_scale=True (src/quantizer.py:516-524,535-536) against the reference's outputs,
+    an all-zero tensor (tensor scale 1) included."""
+    q = _mx(MXCFG[name], per_tensor_scale=True)
+    for key, ref in (("x_f16", f"{name}_pts_f16"), ("x_f32", f"{name}_pts_f32"),
+                     ("x_zero_f16", f"{name}_pts_zero_f16")):
+        dt = "f32" if key == "x_f32" else "f16"
+        x = (torch.from_numpy(golden_extra[key]) if dt == "f32" else to_torch(golden_extra[key], dt)).to(gpu)
+        assert mismatches(to_bits(q.q(x)), golden_extra[ref], dt) == 0, key
 
 
 def test_hbq_golden_ragged(gpu, golden_hbq):
     x = to_torch(golden_hbq["x_ragged_f16"], "f16").to(gpu)
-    y = _hbq(HBQCFG["hbq_a_act"]).q(x)
+    y = _hbq(HBQCFG["hbq_a_act"], use_quant_kernel=False).q(x)
     assert mismatches(to_bits(y), golden_hbq["hbq_a_act_ragged_f16"], "f16") == 0
 
 
@@ -139,13 +167,14 @@ def _edge_rows(x):
 
 @pytest.mark.parametrize("name", list(HBQCFG))
 @pytest.mark.parametrize("dt", ["f16", "bf16", "f32"])
-def test_hbq_vs_oracle(gpu, oracle, name, dt):
-    """HBQ on a 256 x 4096 mixture with edge rows, all dtypes, against the oracle."""
-    print(f"hbq oracle {name} {dt}", flush=True)
+@pytest.mark.parametrize("uqk", [True, False])
+def test_hbq_vs_oracle(gpu, oracle, name, dt, uqk):
+    """HBQ on a 256 x 4096 mixture with edge rows, all dtypes, both element roundings, against the oracle."""
+    print(f"hbq oracle {name} {dt} use_quant_kernel={uqk}", flush=True)
     x = _edge_rows(synth(256, 4096, 11, dt))
-    q = _hbq(HBQCFG[name], keep_l2_scale=True)
+    q = _hbq(HBQCFG[name], keep_l2_scale=True, use_quant_kernel=uqk)
     y = q.q(x.to(gpu))
-    ref = oracle.hbq_qdq(to_bits(x), dt, block_size=128, **HBQCFG[name])
+    ref = oracle.hbq_qdq(to_bits(x), dt, block_size=128, use_quant_kernel=uqk, **HBQCFG[name])
     assert mismatches(to_bits(y), ref["y"], dt) == 0
     assert mismatches(to_bits(q.shared_scale), ref["l1"], dt) == 0
     assert np.array_equal(q.l2_scale.cpu().numpy(), ref["l2idx"].astype(np.int64))
@@ -154,12 +183,13 @@ def test_hbq_vs_oracle(gpu, oracle, name, dt):
 
 @pytest.mark.parametrize("name", list(MXCFG))
 @pytest.mark.parametrize("dt", ["f16", "f32"])
-def test_mxfp_vs_oracle(gpu, oracle, name, dt):
-    print(f"mxfp oracle {name} {dt}", flush=True)
+@pytest.mark.parametrize("dyn", [False, True])
+def test_mxfp_vs_oracle(gpu, oracle, name, dt, dyn):
+    print(f"mxfp oracle {name} {dt} activate_dynamo={dyn}", flush=True)
     x = _edge_rows(synth(256, 4096, 12, dt))
-    q = _mx(MXCFG[name])
+    q = _mx(MXCFG[name], activate_dynamo=dyn)
     out = q.quantize(x.to(gpu))
-    y, s = oracle.mxfp_qdq(to_bits(x), dt, **MXCFG[name])
+    y, s = oracle.mxfp_qdq(to_bits(x), dt, compiled=dyn, **MXCFG[name])
     assert mismatches(to_bits(out.y), y, dt) == 0
     assert mismatches(to_bits(out.scales), s, dt) == 0
 
@@ -241,12 +271,13 @@ def test_hbq_3d_input(gpu, oracle):
 
 @pytest.mark.parametrize("name", ["hbq_a_act", "hbq_a_wgt", "hbq_e_act", "hbq_e_wgt", "hbq_kv4", "hbq_a_wgt_ceil"])
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
-def test_hbq_table_kernel_equals_generic(gpu, name, dt):
+@pytest.mark.parametrize("uqk", [True, False])
+def test_hbq_table_kernel_equals_generic(gpu, name, dt, uqk):
     """The table-driven kernel and the generic kernel agree bit for bit, codes and scales included."""
     from hbq_amd import _lib
-    print(f"fast vs generic {name} {dt}", flush=True)
+    print(f"fast vs generic {name} {dt} use_quant_kernel={uqk}", flush=True)
     x = _edge_rows(synth(512, 4096, 17, dt)).to(gpu)
-    q = _hbq(HBQCFG[name])
+    q = _hbq(HBQCFG[name], use_quant_kernel=uqk)
     fast = q.quantize(x)
     old = _lib.lib().hbq_set_generic_only(1)
     try:
@@ -267,17 +298,18 @@ MXFAST = dict(MXCFG, e2m2_pot=dict(block_size=32, ebit=2, mbit=2, sc_ebit=8, sc_
 
 
 @pytest.mark.parametrize("name", list(MXFAST))
-def test_mxfp_table_kernel_equals_generic(gpu, name):
+@pytest.mark.parametrize("dyn", [False, True])
+def test_mxfp_table_kernel_equals_generic(gpu, name, dyn):
     """The table-driven MXFP / NVFP kernel (fp16, whole blocks) and the generic kernel agree
     bit for bit on outputs, codes and scales, edge rows (zeros, +-inf, NaN, huge, subnormal,
     quotients in the fp16 subnormal range) included."""
     from hbq_amd import _lib
-    print(f"mx fast vs generic {name}", flush=True)
+    print(f"mx fast vs generic {name} activate_dynamo={dyn}", flush=True)
     x = _edge_rows(synth(512, 4096, 18, "f16"))
     x[6] = x[6] * 1e-3            # blocks whose quotients reach the fp16 subnormal range
     x[7, ::3] = 0.0
     xg = x.to(gpu)
-    q = _mx(MXFAST[name])
+    q = _mx(MXFAST[name], activate_dynamo=dyn)
     fast = q.quantize(xg)
     old = _lib.lib().hbq_set_generic_only(1)
     try:

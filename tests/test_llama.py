@@ -75,7 +75,7 @@ def test_quantization_points_match_oracle(gpu, oracle):
         xs = to_bits(x.reshape(-1, x.shape[-1]))
         ref = oracle.hbq_qdq(xs, "f16", block_size=qz.block_size, ebit=qz.ebit, mbit=qz.mbit, sc_ebit=qz.sc_ebit,
                              sc_mbit=qz.sc_mbit, l2_block_size=qz.l2_block_size, l2_sc_bit=qz.l2_sc_bit,
-                             l2_scheme=qz.l2_scheme)["y"]
+                             l2_scheme=qz.l2_scheme, use_quant_kernel=qz._fused)["y"]
         assert mismatches(to_bits(y.reshape(-1, y.shape[-1])), ref, "f16") == 0
         kinds.add((qz.mbit, tuple(x.shape[-2:]) if x.dim() == 4 else "x"))
     # X of the projections (q/k/v and gate/up share one quantized copy), Q (E2M2), K and V

@@ -56,22 +56,96 @@ def test_mxfp_golden(oracle, golden_mxfp, name):
 
 @pytest.mark.parametrize("name", list(HBQCFG))
 @pytest.mark.parametrize("inp", ["f16", "f16w", "bf16"])
-def test_hbq_golden(oracle, golden_hbq, name, inp):
+def test_hbq_golden(oracle, golden_hbq, golden_extra, name, inp):
     key = f"{name}_{inp}"
-    if key not in golden_hbq:
-        pytest.skip("no fixture")
+    fx = golden_hbq if key in golden_hbq.files else golden_extra
     dt = "bf16" if inp == "bf16" else "f16"
-    r = oracle.hbq_qdq(golden_hbq[f"x_{inp}"], dt, block_size=128, **HBQCFG[name])
-    assert mismatches(r["y"], golden_hbq[key], dt) == 0
-    assert mismatches(r["l1"], golden_hbq[key + "_l1"], dt) == 0
-    assert np.array_equal(r["l2idx"], golden_hbq[key + "_l2idx"])
-    assert np.array_equal(r["scheme"], golden_hbq[key + "_scheme"])
-    assert mismatches(r["l2val"], golden_hbq[key + "_l2val"], dt) == 0
+    r = oracle.hbq_qdq(golden_hbq[f"x_{inp}"], dt, block_size=128, use_quant_kernel=False, **HBQCFG[name])
+    assert mismatches(r["y"], fx[key], dt) == 0
+    assert mismatches(r["l1"], fx[key + "_l1"], dt) == 0
+    assert np.array_equal(r["l2idx"], fx[key + "_l2idx"])
+    assert np.array_equal(r["scheme"], fx[key + "_scheme"])
+    assert mismatches(r["l2val"], fx[key + "_l2val"], dt) == 0
 
 
 def test_hbq_golden_ragged(oracle, golden_hbq):
-    r = oracle.hbq_qdq(golden_hbq["x_ragged_f16"], "f16", block_size=128, **HBQCFG["hbq_a_act"])
+    r = oracle.hbq_qdq(golden_hbq["x_ragged_f16"], "f16", block_size=128, use_quant_kernel=False,
+                       **HBQCFG["hbq_a_act"])
     assert mismatches(r["y"], golden_hbq["hbq_a_act_ragged_f16"], "f16") == 0
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("em", [(2, 1), (2, 2), (2, 5)])
+def test_elem_quant_compiled_golden_exhaustive(oracle, golden_compiled, golden_elem, dt, em):
+    """The torch.compile'd make_fp_quant (GLOBAL_FP_QUANT_CACHE, src/quantizer.py:38-63) over
+    every 16-bit pattern.  It differs from the eager function on exactly the values whose
+    |m| + 0.5004 rounds across an integer in T but not in fp32: per format 3 positive fp16
+    values (and their negatives), 1 bf16 value (and its negative)."""
+    key = f"elem_{dt}_e{em[0]}m{em[1]}"
+    assert not bool(golden_compiled["compile_fell_back"])
+    y = oracle.elem_quant(ALL16, dt, *em, compiled=True)
+    assert mismatches(y, golden_compiled[key], dt) == 0
+    diff = mismatches(golden_compiled[key], golden_elem[key], dt)
+    assert diff == (6 if dt == "f16" else 2)
+    # the eager rule would fail here: the compiled oracle is not the eager one renamed
+    assert mismatches(oracle.elem_quant(ALL16, dt, *em), golden_compiled[key], dt) == diff
+
+
+@pytest.mark.parametrize("name", list(HBQCFG))
+@pytest.mark.parametrize("inp", ["f16", "f16w", "bf16"])
+def test_hbq_compiled_golden(oracle, golden_compiled, golden_hbq, name, inp):
+    """HBQQuantizer(use_quant_kernel=True).q, what PTQ builds for every HBQ quantizer
+    (src/ptq.py:144-157,198-211; src/quantizer.py:468-469,724)."""
+    key = f"{name}_{inp}"
+    dt = "bf16" if inp == "bf16" else "f16"
+    r = oracle.hbq_qdq(golden_hbq[f"x_{inp}"], dt, block_size=128, use_quant_kernel=True, **HBQCFG[name])
+    assert mismatches(r["y"], golden_compiled[key], dt) == 0
+    assert mismatches(r["l1"], golden_compiled[key + "_l1"], dt) == 0
+    assert np.array_equal(r["l2idx"], golden_compiled[key + "_l2idx"])
+    assert np.array_equal(r["scheme"], golden_compiled[key + "_scheme"])
+
+
+def test_hbq_compiled_differs_from_eager(golden_compiled, golden_hbq):
+    """How many HBQ outputs the element rule changes on the fixture tensors (32 x 1024 each).
+    Both rules are real: the reference picks one by use_quant_kernel."""
+    total = 0
+    for name in HBQCFG:
+        for inp in ("f16", "f16w", "bf16"):
+            key = f"{name}_{inp}"
+            if key in golden_hbq.files:
+                dt = "bf16" if inp == "bf16" else "f16"
+                total += mismatches(golden_compiled[key], golden_hbq[key], dt)
+    assert total > 0
+    print("HBQ outputs that differ between the compiled and eager element rule:", total)
+
+
+@pytest.mark.parametrize("name", ["mxfp4", "mxfp8", "nvfp4"])
+def test_mxfp_compiled_golden(oracle, golden_compiled, golden_mxfp, name):
+    """MXFPQuantizer(activate_dynamo=True).q (src/quantizer.py:464-466)."""
+    y, _ = oracle.mxfp_qdq(golden_mxfp["x_f16"], "f16", compiled=True, **MXCFG[name])
+    assert mismatches(y, golden_compiled[f"{name}_f16"], "f16") == 0
+    y, _ = oracle.mxfp_qdq(golden_mxfp["x_f32"], "f32", compiled=True, **MXCFG[name])
+    assert mismatches(y, golden_compiled[f"{name}_f32"], "f32") == 0
+
+
+def _tensor_scale(x, ebit, mbit, sc_ebit, sc_mbit):
+    """MXFPQuantizer.q's per-tensor scale (src/quantizer.py:516-524): a Python float."""
+    ele_max = {1: 6.0, 2: 7.0, 5: 7.875}[mbit]
+    sc_max = 61440.0 if (sc_ebit, sc_mbit) == (5, 3) else 2.0 ** ((1 << (sc_ebit - 1)) - 1)
+    x_max = float(np.abs(x).max())
+    return 1.0 if x_max == 0 else x_max / (ele_max * sc_max)
+
+
+@pytest.mark.parametrize("name", ["nvfp4", "mxfp4"])
+def test_mxfp_per_tensor_scale_golden(oracle, golden_extra, name):
+    """The per_tensor_scale=True branch (src/quantizer.py:516-524,535-536), off in every
+    configuration but part of the interface."""
+    for dt, key in (("f16", "x_f16"), ("f32", "x_f32"), ("f16", "x_zero_f16")):
+        xb = golden_extra[key]
+        ts = _tensor_scale(as_float(xb, dt), 2, MXCFG[name]["mbit"], MXCFG[name]["sc_ebit"], MXCFG[name]["sc_mbit"])
+        y, _ = oracle.mxfp_qdq(xb, dt, tensor_scale=ts, **MXCFG[name])
+        ref = golden_extra[f"{name}_pts_zero_f16" if key == "x_zero_f16" else f"{name}_pts_{dt}"]
+        assert mismatches(y, ref, dt) == 0, (name, key)
 
 
 # ---------------------------------------------------------------------------
@@ -180,12 +254,14 @@ def test_scale_quant_closed_form(oracle, use_ceil):
     assert np.array_equal(got[quirk], e1 * (1.125 if use_ceil else 1.0))
 
 
-def test_hbq_without_l2_equals_nvfp(oracle):
+@pytest.mark.parametrize("compiled", [False, True])
+def test_hbq_without_l2_equals_nvfp(oracle, compiled):
     """HBQ with one L2 candidate (l2_sc_bit=0, factor 1) is the FP-scale MX path: both run
     fp_quant(clip(amax / ele_max)) and the same element rounding (src/quantizer.py:505-509, 736-738)."""
     x = to_bits(synth(32, 512, 3, "f16"))
-    h = oracle.hbq_qdq(x, "f16", block_size=128, ebit=2, mbit=1, l2_block_size=4, l2_sc_bit=0, l2_scheme="PoT")
-    y, s = oracle.mxfp_qdq(x, "f16", block_size=128, ebit=2, mbit=1, sc_ebit=5, sc_mbit=3)
+    h = oracle.hbq_qdq(x, "f16", block_size=128, ebit=2, mbit=1, l2_block_size=4, l2_sc_bit=0, l2_scheme="PoT",
+                       use_quant_kernel=compiled)
+    y, s = oracle.mxfp_qdq(x, "f16", block_size=128, ebit=2, mbit=1, sc_ebit=5, sc_mbit=3, compiled=compiled)
     assert mismatches(h["y"], y, "f16") == 0
     assert mismatches(h["l1"], s, "f16") == 0
 
@@ -235,7 +311,7 @@ def test_hbq_choice_is_near_optimal_exactly(oracle):
             errs = np.zeros((16, 4), dtype=object)
             for j in range(4):
                 u = t / torch.tensor(float(tab[j, s])).half()
-                q = as_float(oracle.elem_quant(to_bits(u), "f16", 2, 1), "f16")
+                q = as_float(oracle.elem_quant(to_bits(u), "f16", 2, 1, compiled=True), "f16")
                 d = [Fraction(float(v)) * Fraction(float(tab[j, s])) * Fraction(l1) for v in q]
                 e2 = [(Fraction(float(a)) - b) ** 2 for a, b in zip(xr.numpy(), d)]
                 for u_ in range(16):
@@ -268,18 +344,132 @@ def test_gemm_ones_closed_form(oracle):
     assert np.all(as_float(oracle.gemm_fp32_accum(A, B), "f16") == K)
 
 
-def test_grouped_fp16_rounding_closed_form(oracle):
-    """Group partials 2049 (fp16 rounds to 2048 then 2048 + 2048 ...): the grouped result is
-    the fp16 running sum of fp16-rounded partials, not the exact total."""
-    K, gk = 3 * 128, 128
-    A = _h(np.full((1, K), 16.0))
-    B = np.full((K, 1), 1.0)
-    B[0] = 17.0                                 # group 0: 16*127 + 16*17 = 2304; others 2048
-    C = as_float(oracle.gemm_fp16_grouped_accum(A, _h(B), gk), "f16")[0, 0]
-    h = np.float16(0)
-    for p in (2304.0, 2048.0, 2048.0):
-        h = np.float16(h + np.float16(p))
-    assert C == float(h)
+def _partials_gemm(partials, gk, tail=None):
+    """A [1, K] and B [K, N] whose K groups of gk have the given fp32 partials per column:
+    A = 1 and one nonzero B entry per (group, column).  Every partial must be an fp16 value,
+    so each group partial is exact whatever the sum order inside the group.  tail: length
+    of a ragged last group (K = (G - 1) gk + tail)."""
+    P = np.asarray(partials, np.float64)
+    G, N = P.shape
+    K = (G - 1) * gk + (tail if tail else gk)
+    A = np.ones((1, K))
+    B = np.zeros((K, N))
+    for g in range(G):
+        B[g * gk] = P[g]
+    assert np.array_equal(np.float16(B).astype(np.float64), B)
+    return _h(A), _h(B)
+
+
+def test_grouped_cross_group_sum_is_fp16(oracle):
+    """Group partials 2048, 1, 1: the fp16 running sum gives 2048 (2048 + 1 is a tie that
+    rounds to even, twice); an fp32 running sum, or one sum rounded at the end, gives 2050
+    (gemm.cu:354-377: H = R16(H + R16(P)) per group in ascending order)."""
+    for gk in (16, 32, 64, 128):
+        A, B = _partials_gemm([[2048.0], [1.0], [1.0]], gk)
+        assert as_float(oracle.gemm_fp16_grouped_accum(A, B, gk), "f16")[0, 0] == 2048.0
+    # and a tail group of 8 after two full groups of 16 is its own group: merging it into
+    # group 1 (partials 2048, 2) would give 2050
+    A, B = _partials_gemm([[2048.0], [1.0], [1.0]], 16, tail=8)
+    assert as_float(oracle.gemm_fp16_grouped_accum(A, B, 16), "f16")[0, 0] == 2048.0
+
+
+def test_grouped_partial_rounded_before_add(oracle):
+    """Partials 2050 then 2049: R16(2049) = 2048 (tie to even) and 2050 + 2048 = 4098 is a
+    tie that rounds to 4096.  Adding the unrounded 2049 (4099) would round to 4100, and so
+    would an fp32 running sum."""
+    gk = 32
+    # 2049 is not an fp16 value: group 1 holds 2048 + 1 (two B entries, exact in fp32)
+    K = 2 * gk
+    A = np.ones((1, K))
+    B = np.zeros((K, 1))
+    B[0, 0] = 2050.0
+    B[gk, 0] = 2048.0
+    B[gk + 1, 0] = 1.0
+    C = as_float(oracle.gemm_fp16_grouped_accum(_h(A), _h(B), gk), "f16")[0, 0]
+    assert C == 4096.0
+
+
+def test_fp32_accum_is_sequential_fp32(oracle):
+    """gemm_fp32_accum keeps one fp32 accumulator over ascending k (gemm.cu:96-303).  fp16 x
+    fp16 products are exact in fp32 (22 significant bits), so fusing the multiply cannot
+    change a step; what this pins is the fp32 accumulator and the order:
+    4 x 2^22, then 1, 1, then 4 x -2^22: 2^24 + 1 is a tie that stays 2^24, twice, so the sum
+    is 0.  Exact or double accumulation gives 2, and so does the descending order."""
+    a = np.array([2048.0] * 4 + [1.0, 1.0] + [2048.0] * 4)
+    b = np.array([2048.0] * 4 + [1.0, 1.0] + [-2048.0] * 4)
+    A, B = _h(a[None, :]), _h(b[:, None])
+    assert as_float(oracle.gemm_fp32_accum(A, B), "f16")[0, 0] == 0.0
+    A, B = _h(a[None, ::-1]), _h(b[::-1, None])
+    assert as_float(oracle.gemm_fp32_accum(A, B), "f16")[0, 0] == 2.0
+
+
+def test_mxint8_multi_group_known_answer(oracle):
+    """Two groups of gk = 64, GN = 4, through the whole GEMM (gemm.cu:1198-1277).
+    Group 0 partials [100.75, -3.5, 2.5, 0.5]: s = 2^(ilogb(100.75) - 6) = 1, rne -> [101, -4, 2, 0].
+    Group 1 partials [1000, 1, -1020, 4]: s = 2^(9 - 6) = 8; -1020/8 = -127.5 -> -128 -> clamp
+    -127 -> -1016; 1/8 and 4/8 -> 0.  H = [1101, -4, -1014, 0].  Quantizing the running sum
+    instead (max 1101, s = 16) would give [1104, 0, -1024, 0]."""
+    A, B = _partials_gemm([[100.75, -3.5, 2.5, 0.5], [1000.0, 1.0, -1020.0, 4.0]], 64)
+    C = as_float(oracle.gemm_blockquant_mxint8(A, B, 64, 4), "f16")[0]
+    assert list(C) == [1101.0, -4.0, -1014.0, 0.0]
+
+
+def test_mxfp8_multi_group_known_answer(oracle):
+    """Two groups of gk = 64, GN = 4 (gemm.cu:669-745, 1040-1135).
+    Group 0 [10, 1.03125, 0.2001953125, -0.00390625]: s = 2^(3 - 3) = 1; 10 -> 10,
+    1.03125 -> 1 (mantissa 0.5 rounds to even 0), 0.2002 -> 13/64, 2^-8 < 2^-7 -> +0.
+    Group 1 [-20, 0.375, 100, 3]: s = 2^(6 - 3) = 8; each value is on the E3M4 grid there.
+    H = [-10, 1.375, R16(0.203125 + 100) = 100.1875, 3]."""
+    P = [[10.0, 1.03125, 0.2001953125, -0.00390625], [-20.0, 0.375, 100.0, 3.0]]
+    A, B = _partials_gemm(P, 64)
+    C = as_float(oracle.gemm_blockquant_mxfp8(A, B, 64, 4), "f16")[0]
+    assert list(C) == [-10.0, 1.375, 100.1875, 3.0]
+
+
+@pytest.mark.parametrize("op", ["fp32", "fp16", "grouped", "mxint8", "mxfp8"])
+def test_gemm_oracle_within_float64_bound(oracle, op):
+    """Every oracle GEMM against the float64 product, within the bound its rounding steps
+    allow (S = sum_k |a_k b_k| per output, G groups, u_h = 2^-11, u_f = 2^-24):
+      fp32:    K u_f S + u_h |C|                        (fp32 chain, one fp16 rounding)
+      fp16:    K u_h S                                  (one fp16 rounding per step)
+      grouped: (gk u_f + (2G + 1) u_h) S                (partials, their fp16 roundings, the adds)
+      mxint8/mxfp8: the grouped bound plus G times half the psum step, max|P_g| 2^-7
+               (int8: s/2 = 2^(ilogb - 7)) or 2^-5 (E3M4: 2^(ilogb - 3) spacing / 2 at 15.5).
+    A transposed operand, a dropped group or a wrong scale breaks the bound by orders of
+    magnitude on this data."""
+    rng = np.random.default_rng(5)
+    M, K, N, gk, gn = 8, 512, 64, 128, 32
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    B = (rng.standard_normal((K, N)) * 0.05).astype(np.float16)
+    Ab, Bb = A.view(np.uint16), B.view(np.uint16)
+    Ad, Bd = A.astype(np.float64), B.astype(np.float64)
+    ref = Ad @ Bd
+    S = np.abs(Ad) @ np.abs(Bd)
+    G = K // gk
+    uh, uf = 2.0 ** -11, 2.0 ** -24
+    if op == "fp32":
+        C, bound = oracle.gemm_fp32_accum(Ab, Bb), K * uf * S + uh * np.abs(ref)
+    elif op == "fp16":
+        C, bound = oracle.gemm_fp16_accum(Ab, Bb), K * uh * S
+    else:
+        bound = (gk * uf + (2 * G + 1) * uh) * S
+        if op == "grouped":
+            C = oracle.gemm_fp16_grouped_accum(Ab, Bb, gk)
+        else:
+            P = np.stack([Ad[:, g * gk:(g + 1) * gk] @ Bd[g * gk:(g + 1) * gk] for g in range(G)])
+            pmax = np.abs(P).reshape(G, M, N // gn, gn).max(-1).repeat(gn, axis=-1).sum(0)
+            step = 2.0 ** -7 if op == "mxint8" else 2.0 ** -5
+            bound = bound + step * pmax * 1.01
+            f = oracle.gemm_blockquant_mxint8 if op == "mxint8" else oracle.gemm_blockquant_mxfp8
+            C = f(Ab, Bb, gk, gn)
+    err = np.abs(as_float(C, "f16").astype(np.float64) - ref)
+    assert np.all(err <= bound), float((err / bound).max())
+    # the bound is not vacuous: a transposed B (square blocks) lands far outside it
+    if op == "grouped":
+        Bt = np.ascontiguousarray(B[:N, :].T.astype(np.float16))
+        Bt = np.concatenate([Bt] * (K // N), axis=0).astype(np.float16)
+        Cbad = as_float(oracle.gemm_fp16_grouped_accum(Ab, Bt.view(np.uint16), gk), "f16")
+        assert np.any(np.abs(Cbad.astype(np.float64) - ref) > bound)
 
 
 def test_mxint8_epilogue_known_answer(oracle):
