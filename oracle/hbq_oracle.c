@@ -557,14 +557,20 @@ static float hfma(uint16_t a, uint16_t b, uint16_t c) {
     return neg ? -(float)val : (float)val;
 }
 
+/* One fp32 fmaf chain per output over ascending k.  The loops run k outside n so B is
+ * read along its rows; each output's chain keeps its own order (loop interchange only). */
 int orc_gemm_fp32acc(const uint16_t *A, const uint16_t *B, uint16_t *C, int M, int N, int K) {
 #pragma omp parallel for schedule(static)
-    for (int m = 0; m < M; ++m)
-        for (int n = 0; n < N; ++n) {
-            float acc = 0.f;
-            for (int k = 0; k < K; ++k) acc = fmaf(h2f(A[(int64_t)m * K + k]), h2f(B[(int64_t)k * N + n]), acc);
-            C[(int64_t)m * N + n] = f2h(acc);
+    for (int m = 0; m < M; ++m) {
+        float *acc = calloc((size_t)N, sizeof(float));
+        for (int k = 0; k < K; ++k) {
+            const float a = h2f(A[(int64_t)m * K + k]);
+            const uint16_t *b = B + (int64_t)k * N;
+            for (int n = 0; n < N; ++n) acc[n] = fmaf(a, h2f(b[n]), acc[n]);
         }
+        for (int n = 0; n < N; ++n) C[(int64_t)m * N + n] = f2h(acc[n]);
+        free(acc);
+    }
     return 0;
 }
 
@@ -675,16 +681,30 @@ int orc_epilogue(const float *P, uint16_t *C, int G, int M, int N, int mode, int
     return 0;
 }
 
-/* group partials P[g][m][n] with groups of gk along K; the tail group ends at K */
+/* group partials P[g][m][n] with groups of gk along K; the tail group ends at K.  Each
+ * partial is group_partial()'s sequential fmaf chain; the loops run k outside n so B is
+ * read along its rows (loop interchange only: every chain keeps its ascending order). */
 int orc_group_partials(const uint16_t *A, const uint16_t *B, float *P, int M, int N, int K, int gk) {
     int G = (K + gk - 1) / gk;
 #pragma omp parallel for schedule(static)
     for (int m = 0; m < M; ++m)
         for (int g = 0; g < G; ++g) {
             int k0 = g * gk, k1 = k0 + gk < K ? k0 + gk : K;
-            for (int n = 0; n < N; ++n) P[((int64_t)g * M + m) * N + n] = group_partial(A, B, N, K, m, n, k0, k1);
+            float *p = P + ((int64_t)g * M + m) * N;
+            for (int n = 0; n < N; ++n) p[n] = 0.f;
+            for (int k = k0; k < k1; ++k) {
+                const float a = h2f(A[(int64_t)m * K + k]);
+                const uint16_t *b = B + (int64_t)k * N;
+                for (int n = 0; n < N; ++n) p[n] = fmaf(a, h2f(b[n]), p[n]);
+            }
         }
     return 0;
+}
+
+/* the partial of one (m, n): kept as the plain statement of the chain above; the tests
+ * compare both */
+float orc_group_partial_one(const uint16_t *A, const uint16_t *B, int N, int K, int m, int n, int k0, int k1) {
+    return group_partial(A, B, N, K, m, n, k0, k1);
 }
 
 static int gemm_grouped_mode(const uint16_t *A, const uint16_t *B, uint16_t *C, int M, int N, int K, int gk,

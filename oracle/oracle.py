@@ -53,6 +53,8 @@ def lib():
         L.orc_cascade_sum.restype = ctypes.c_float
         L.orc_row_sum.argtypes = [P, I64]
         L.orc_row_sum.restype = ctypes.c_float
+        L.orc_group_partial_one.argtypes = [P, P, I, I, I, I, I, I]
+        L.orc_group_partial_one.restype = ctypes.c_float
         for name, args in sig.items():
             fn = getattr(L, name)
             fn.argtypes = args
@@ -233,6 +235,12 @@ def group_partials(A, B, group_k):
     P = np.empty((G, M, N), np.float32)
     _check(lib().orc_group_partials(_p(A), _p(B), _p(P), M, N, K, group_k), "group_partials")
     return P
+
+
+def group_partial_one(A, B, m, n, k0, k1):
+    """One fp32 partial, the sequential chain written per output (for checking group_partials)."""
+    A, B, _ = _gemm_in(A, B)
+    return float(lib().orc_group_partial_one(_p(A), _p(B), B.shape[1], A.shape[1], m, n, k0, k1))
 
 
 def epilogue(P, mode, group_n=0):

@@ -504,6 +504,20 @@ def test_fp16_chain_is_fused(oracle):
             assert C[m, n] == float(h)
 
 
+def test_group_partials_loop_order_is_per_output_chain(oracle):
+    """orc_group_partials runs k outside n for speed; each output must still be the
+    per-output sequential chain, bit for bit, including a ragged tail group."""
+    rng = np.random.default_rng(3)
+    A = (rng.standard_normal((3, 200)) * 4).astype(np.float16)
+    B = (rng.standard_normal((200, 5)) * 0.1).astype(np.float16)
+    P = oracle.group_partials(A.view(np.uint16), B.view(np.uint16), 64)
+    for g in range(4):
+        for m in range(3):
+            for n in range(5):
+                one = oracle.group_partial_one(A.view(np.uint16), B.view(np.uint16), m, n, 64 * g, min(64 * g + 64, 200))
+                assert np.float32(one) == P[g, m, n]
+
+
 def test_group_partials_sequential_fmaf(oracle):
     """Group partials equal a sequential fused fp32 chain (fmaf via exact rationals)."""
     rng = np.random.default_rng(1)
