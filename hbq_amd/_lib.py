@@ -26,6 +26,7 @@ SIGNATURES = {
     "hbq_scale_quant": ([_P, _P, _I64, _I, _I, _I, _I, _I, _I, _P], _I),
     "hbq_gemm_fp32_accum_workspace": ([_I64, _I64, _I64, _I], _I64),
     "hbq_gemm_fp32_accum_ws": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P], _I),
+    "hbq_gemm_fp32_accum_noalloc": ([_P, _P, _P, _I64, _I64, _I64, _I, _P], _I),
     "hbq_gemm_fp32_accum_batched": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P], _I),
     "hbq_gemm_fp32_accum": ([_P, _P, _P, _I64, _I64, _I64, _I, _P], _I),
     "hbq_gemm_fp16_accum": ([_P, _P, _P, _I64, _I64, _I64, _I, _P], _I),

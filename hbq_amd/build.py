@@ -15,6 +15,7 @@ from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")   # the public C ABI header
 OUT_DIR = os.path.join(HERE, "_lib")
 LIB = os.path.join(OUT_DIR, "libhbq_amd.so")
 ARCH = os.environ.get("HBQ_OFFLOAD_ARCH", "gfx950")
@@ -34,7 +35,7 @@ def hipcc():
 
 def _compile(args):
     src, obj, flags = args
-    cmd = [hipcc()] + COMMON + flags + ["-I", CSRC, "-c", src, "-o", obj]
+    cmd = [hipcc()] + COMMON + flags + ["-I", CSRC, "-I", INCLUDE, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

@@ -18,11 +18,13 @@
 // output element, so they give the same bits.
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include <mutex>
 #include <stdint.h>
 
 #include "gemm_common.h"
 #include "gemm_tile256.h"
 #include "hbq_capi_internal.h"
+#include "hbq_amd.h"
 
 namespace hbq_gemm {
 
@@ -381,9 +383,66 @@ int zero_output(void* C, int64_t M, int64_t N, hipStream_t st) {
     return 0;
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free entry point (hbq_gemm_fp32_accum_noalloc): the
+// split-K fp32 partials in a file-scope device array, one copy on every GPU the
+// library runs on, held until the process ends.  Its name is a host-side stand-in
+// for the symbol, not a device address: host code takes each device's address from
+// hipGetSymbolAddress (first call on that device, with it current) and passes that.
+// The split kernel writes every partial of the shape before the sum reads it, so
+// nothing needs clearing between calls; calls that overlap on one GPU race on it.
+// ---------------------------------------------------------------------------
+constexpr int64_t kNoAllocScratchBytes = HBQ_NOALLOC_SCRATCH_BYTES;   // 2 splits x 2048 x 4096 fp32
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kScratchDevices];
+
+int scratch_ptr(float** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hbq_fail(HBQ_ERR_HIP, "hipGetDevice failed: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kScratchDevices) return hbq_fail(HBQ_ERR_UNSUPPORTED, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr)
+            return hbq_fail(HBQ_ERR_HIP, "hipGetSymbolAddress of the scratch buffer failed: %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = (float*)p;
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+
 }  // namespace
 
 extern "C" {
+
+int hbq_gemm_fp32_accum_noalloc(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+                                int b_is_nk, void* stream) {
+    hbq_clear_error();
+    if (int rc = check_shapes(A, B, C, M, N, K)) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    if (M == 0 || N == 0) return 0;
+    if (K == 0) return zero_output(C, M, N, st);
+    const int64_t need = hbq_gemm_fp32_accum_workspace(M, N, K, b_is_nk);
+    if (need > kNoAllocScratchBytes)
+        return hbq_fail(HBQ_ERR_INVALID,
+                        "gemm_fp32_accum_noalloc: the split-K partials of this shape take %lld bytes, more than the "
+                        "%lld-byte scratch buffer (use hbq_gemm_fp32_accum_ws with a workspace)",
+                        (long long)need, (long long)kNoAllocScratchBytes);
+    if (need > 0) {
+        float* ws = nullptr;
+        if (int rc = scratch_ptr(&ws)) return rc;
+        if (launch_splitk_fp32(A, B, C, ws, (int)M, (int)N, (int)K,
+                               (int)(need / ((int64_t)sizeof(float) * M * N)), st))
+            return hbq_check_launch("gemm_fp32_accum_noalloc (split K)");
+    }
+    launch_any<kFp32, 4>(A, B, C, nullptr, (int)M, (int)N, (int)K, (int)K, b_is_nk, st);
+    return hbq_check_launch("gemm_fp32_accum_noalloc");
+}
 
 int hbq_gemm_fp32_accum(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int b_is_nk,
                         void* stream) {

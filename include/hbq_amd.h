@@ -203,6 +203,19 @@ int64_t hbq_gemm_fp32_accum_workspace(int64_t M, int64_t N, int64_t K, int b_is_
 int hbq_gemm_fp32_accum_ws(const void *A, const void *B, void *C, void *ws, int64_t ws_bytes, int64_t M, int64_t N,
                            int64_t K, int b_is_nk, void *stream);
 
+/* No reference counterpart: hbq_gemm_fp32_accum_ws for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * It allocates nothing and takes no workspace: the split-K partials live in a
+ * library-owned device buffer of HBQ_NOALLOC_SCRATCH_BYTES (64 MiB: the prefill's
+ * down projection, 2 x 2048 x 4096 fp32) on each GPU, held until the process ends.
+ * Same results as hbq_gemm_fp32_accum_ws with a sufficient workspace.  Returns
+ * HBQ_ERR_INVALID when hbq_gemm_fp32_accum_workspace() of the shape exceeds the buffer.
+ * Every call on a GPU shares that GPU's buffer: calls that overlap on one GPU (other
+ * streams, other threads) race and must be serialized by the caller. */
+#define HBQ_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int hbq_gemm_fp32_accum_noalloc(const void *A, const void *B, void *C, int64_t M, int64_t N, int64_t K, int b_is_nk,
+                                void *stream);
+
 /* No reference counterpart: `batches` independent fp32-accumulation GEMMs
  * C_z[M,N] = A_z[M,K] W_z[N,K]^T (fp16, z-th problem at element offsets z * stride_*),
  * the same arithmetic as hbq_gemm_fp32_accum with b_is_nk = 1, in one launch.  The
