@@ -348,19 +348,79 @@ def cpu_model():
     return platform.processor()
 
 
-def cpu_baseline(x_bits_cpu, cfg, bytes_per_elem, reps):
-    """The C oracle (port of the reference op sequence) on the host cores."""
+def quant_inputs(dev=None):
+    """The quantizer inputs of configs[0], [2] and [3] (seeded, fp16): activations N(0, 1) with
+    8 outlier channels x50, the configs[0] weight N(0, 0.02).  Name -> (tensor, format, config)."""
+    g = torch.Generator().manual_seed(2000)
+
+    def act(rows, cols):
+        x = torch.randn(rows, cols, generator=g)
+        x[:, torch.randperm(cols, generator=g)[:8]] *= 50.0
+        return x.half()
+    out = {
+        "cfg0_w_hbq_a_wgt": ((torch.randn(4096, 4096, generator=g) * 0.02).half(), "hbq", HBQ_CFGS["hbq_a_wgt"]),
+        "cfg0_x_hbq_a_act": (act(2048, 4096), "hbq", HBQ_CFGS["hbq_a_act"]),
+        "cfg2_x_hbq_e_act": (act(4096, 4096), "hbq", HBQ_CFGS["hbq_e_act"]),
+        "cfg3_x_hbq_e_act": (act(8192, 4096), "hbq", HBQ_CFGS["hbq_e_act"]),
+        "cfg3_x_nvfp4": (act(8192, 4096), "mx", MX_CFGS["nvfp4"]),
+    }
+    if dev is not None:
+        out = {k: (t.to(dev), f, c) for k, (t, f, c) in out.items()}
+    return out
+
+
+def quant_config_extra(dev, iters=50):
+    """GPU time of the configs[0] / [2] / [3] quantizers (the cpu_baseline's sample), same inputs."""
+    out = {}
+    for name, (x, fmt, cfg) in quant_inputs(dev).items():
+        step, _ = hbq_launcher(x, cfg) if fmt == "hbq" else mx_launcher(x, cfg)
+        for _ in range(3):
+            step()
+        t = HipTimer().run(step, iters)
+        bpe = hbq_bytes_per_elem(cfg) if fmt == "hbq" else mx_bytes_per_elem(cfg)
+        out[f"{name}_us"] = round(t * 1e6, 1)
+        out[f"{name}_GBs"] = round(x.numel() * bpe / t / 1e9, 1)
+    return out
+
+
+def cpu_baseline(x_bits_cpu, cfg, bytes_per_elem, warmup=2, reps=5):
+    """The C oracle (a port of the reference op sequence, OpenMP over rows) on the host cores:
+    median of `reps` runs after `warmup`, for the configs[1] headline quantizer (value) and the
+    quantizers of configs[0], [2] and [3] (by_config)."""
     from oracle import oracle as O
     O.lib()
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[len(ts) // 2]
+
     n = x_bits_cpu.size
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        O.hbq_qdq(x_bits_cpu, "bf16", block_size=128, **cfg)
-    dt = (time.perf_counter() - t0) / reps
+    dt = timed(lambda: O.hbq_qdq(x_bits_cpu, "bf16", block_size=128, **cfg))
+    by_config = {"cfg1_hbq_a_act_bf16": {"ms": round(dt * 1e3, 1), "GBs": round(n * bytes_per_elem / dt / 1e9, 3)}}
+    total = dt * (warmup + reps)
+    for name, (x, fmt, c) in quant_inputs().items():
+        bits = x.contiguous().view(torch.int16).numpy().view("uint16")
+        if fmt == "hbq":
+            t = timed(lambda: O.hbq_qdq(bits, "f16", block_size=128, **c))
+            bpe = hbq_bytes_per_elem(c)
+        else:
+            t = timed(lambda: O.mxfp_qdq(bits, "f16", **c))
+            bpe = mx_bytes_per_elem(c)
+        by_config[name] = {"ms": round(t * 1e3, 1), "GBs": round(x.numel() * bpe / t / 1e9, 3)}
+        total += t * (warmup + reps)
     threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count())
-    return {"value": round(n * bytes_per_elem / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"full configs[1] tensor ({n} bf16 elements), HBQ-A act, {reps} repetitions, "
-                      f"{dt * 1e3:.0f} ms each; {cpu_model()}"}
+    return {"value": by_config["cfg1_hbq_a_act_bf16"]["GBs"], "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"the full configs[1] tensor ({n} bf16 elements), HBQ-A act, median of {reps} runs after "
+                      f"{warmup} warm-ups ({dt * 1e3:.0f} ms); by_config: the same for the configs[0] W and X, "
+                      f"configs[2] and configs[3] quantizers at full size; {total:.1f} s of CPU work in all",
+            "threads": threads, "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+            "cpu_model": cpu_model(), "by_config": by_config}
 
 
 def load_traffic(name):
@@ -446,6 +506,7 @@ def main():
             extra[f"{name}_fp16_frac"] = round(n * mx_bytes_per_elem(c) / t / 1e9 / HBM_PEAK_GBS, 4)
         extra.update(packed_extra(dev))
         if not args.quant_only:
+            extra.update(quant_config_extra(dev))
             extra.update(config0_extra(dev))
             extra.update(gemm_extra(dev))
             extra.update(prefill_extra(dev))
@@ -477,7 +538,7 @@ def main():
     }
     if not (args.quick or args.quant_only):
         bits = x_cpu.contiguous().view(torch.int16).numpy().view("uint16")
-        out["cpu_baseline"] = cpu_baseline(bits, cfg, bpe, reps=2)
+        out["cpu_baseline"] = cpu_baseline(bits, cfg, bpe)
     print(json.dumps(out))
 
 

@@ -4,19 +4,28 @@
 // After the shared scale, the element path of the reference is
 //   u = R16(x / s),  q = lpfp(u),  y = R16(q * s)
 // and lpfp (make_fp_quant, src/quantizer.py:187-257) is a function of the
-// 16-bit value u alone.  So one table indexed by the bits of |u| gives the
-// element level (the magnitude code) and the level's magnitude as fp16, for
-// the binades [2^-(m+2), 2^3) where the level is not constant; below it every
-// u quantizes to level 0, at or above 8 every u saturates.  The table is
-// built on the GPU by the same device element quantizer as the generic kernel
-// (so it agrees with it by construction), its constant ends are checked, and
-// each persistent workgroup copies it into LDS.  Per element what remains is
-// R16(|x| * 1/s) (exact for a power-of-two scale; for the E5M3 scale of NVFP
-// it equals R16(|x| / s) outside the fp16 subnormal range, and the kernel
-// divides where a quotient falls there), one LDS read, R16(q * s) and the
-// sign: the output and the code take the sign of x unless u is +-0, where the
-// reference gives +0 and code 0 (src/quantizer.py:241-245).  A block holding
-// a NaN, or whose scale is 0 or inf in fp16, takes the generic element path.
+// 16-bit value u alone.  So one table of 32-bit words indexed by the bits of |u|
+// gives, in one LDS read, the element level (the magnitude code, low byte) and
+// the level's magnitude as fp16 (high half), for the binades [2^-(m+2), 2^3)
+// where the level is not constant; below it every u quantizes to level 0, at or
+// above 8 every u saturates.  The table is built on the GPU by the same device
+// element quantizer as the generic kernel (so it agrees with it by
+// construction), its constant ends are checked, and each persistent workgroup
+// copies it into LDS.  Per element what remains is R16(|x| * 1/s) (exact for a
+// power-of-two scale; for the E5M3 scale of NVFP it equals R16(|x| / s)
+// outside the fp16 subnormal range, and the kernel divides where a quotient
+// falls there), the LDS read, R16(q * s) and the sign: the output and the code
+// take the sign of x unless u is +-0, where the reference gives +0 and code 0
+// (src/quantizer.py:241-245).  A wave tile holding a NaN, or a block whose
+// scale is 0 or inf in fp16, takes the generic element path.
+//
+// Lane mapping: a wave works on 1024 consecutive elements, lane l holding
+// elements [8 l, 8 l + 8) and [512 + 8 l, 512 + 8 l + 8), so that each of the
+// wave's global load and store instructions covers one contiguous range (1 KB
+// of x or y, 256 / 512 B of codes).  A block (16 or 32 elements) is 2 or 4
+// neighbouring lanes of one half.  A traffic-only kernel streaming y + codes +
+// scales this way measured 6.4 TB/s against 5.1 TB/s with 16 contiguous elements
+// per lane.  Plain (not nontemporal) loads and stores measured slightly faster here.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <mutex>
@@ -29,14 +38,14 @@
 namespace hbq {
 
 constexpr int kMxSlots = 12;   // mbit + 6 * fused
-constexpr int kMxMaxWords = 10 * 1024 + 2;   // E2M5: binades 2^-7 .. 2^3, plus 2 sentinels
-constexpr int kMxMagBytes = 256;             // fp16 magnitudes of up to 128 levels
-constexpr int kMxTabBytes = (kMxMagBytes + kMxMaxWords + 15) / 16 * 16;
+// E2M5: binades 2^-7 .. 2^3 plus 2 sentinels, rounded up so the kernel's 16-byte copy of
+// (n + 2) words stays inside the row and every row starts 16-byte aligned
+constexpr int kMxMaxWords = 10 * 1024 + 8;
+constexpr int kMxThreads = 512;              // 8 waves share one LDS copy of the table
 
-// per slot: bytes [0, 256) the fp16 magnitude of every level; from byte 256 the
-// level of each u: byte 256 + k + 1 for u with fp16 bits lo_bits + k, byte 256
-// below the range (level 0), byte 256 + n + 1 at or above it (saturated)
-static __device__ __attribute__((aligned(16))) uint8_t g_mx_tab[kMxSlots][kMxTabBytes];
+// per slot: word k + 1 for u with fp16 bits lo_bits + k, word 0 below the range
+// (level 0), word n + 1 at or above it (saturated); word = magnitude (fp16) << 16 | level
+static __device__ __attribute__((aligned(16))) uint32_t g_mx_tab[kMxSlots][kMxMaxWords];
 static __device__ int g_mx_status[kMxSlots];
 static __device__ int g_mx_bad[kMxSlots];
 
@@ -56,19 +65,17 @@ __device__ __forceinline__ uint32_t mx_level(float u, float& mag, bool fused) {
 template <int M>
 __global__ void build_mx_lut_kernel(int slot, int n, uint32_t lo_bits, int fused) {
     const int per = n + 2;
-    uint8_t* tab = g_mx_tab[slot];
+    uint32_t* tab = g_mx_tab[slot];
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < per; i += gridDim.x * blockDim.x) {
         float u, mag;
         if (i == 0) u = 0.f;
         else if (i == per - 1) u = 65504.f;   // fp16 max: saturated
         else u = F16::load((uint16_t)(lo_bits + (uint32_t)(i - 1)));
         const uint32_t lv = mx_level<M>(u, mag, fused);
-        tab[kMxMagBytes + i] = (uint8_t)lv;
-        // the table stores one magnitude per level: every u of a level must give it
+        // every u of a level must give the level's own magnitude
         if (F16::store(mag) != F16::store(mx_level_value<M>((int)lv))) atomicMax(&g_mx_bad[slot], 4);
+        tab[i] = ((uint32_t)F16::store(mag) << 16) | lv;
     }
-    const int g = blockIdx.x * blockDim.x + threadIdx.x;
-    if (g < (1 << (M + 2))) reinterpret_cast<uint16_t*>(tab)[g] = F16::store(mx_level_value<M>(g));
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         // the constant ends: the largest value below 2^lo has level 0, 2^hi (the
         // first value above the range) is already saturated
@@ -92,147 +99,206 @@ __device__ __forceinline__ void mix_hi(uint32_t& d, uint32_t h, float f) {
     asm("v_fma_mixhi_f16 %0, |%1|, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(d) : "v"(h), "v"(f));
 }
 
-// LPB lanes of 16 elements per block (block 16 or 32), persistent workgroups
-template <int M, int LPB>
-__global__ __launch_bounds__(kThreads) void mx_fast_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
-                                                           uint16_t* __restrict__ scales, uint8_t* __restrict__ codes,
-                                                           int64_t nb, int slot, int n, uint32_t lo_m1, MxParams p) {
-    constexpr int block = kV * LPB;
-    constexpr int blocks_per_wg = kThreads / LPB;
-    extern __shared__ __attribute__((aligned(16))) uint8_t tab[];
-    {   // copy the table in 16-byte pieces
-        const uint4* src = reinterpret_cast<const uint4*>(g_mx_tab[slot]);
-        uint4* dst = reinterpret_cast<uint4*>(tab);
-        for (int i = threadIdx.x; i < (kMxMagBytes + n + 2 + 15) / 16; i += kThreads) dst[i] = src[i];
+// block max of the 16-bit patterns over the L lanes of a block (L = 2 or 4, aligned)
+template <int L>
+__device__ __forceinline__ uint32_t lanes_max(uint32_t v) {
+    uint32_t o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xf, 0xf, true);   // quad_perm [1,0,3,2]
+    v = v > o ? v : o;
+    if constexpr (L == 4) {
+        o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xf, 0xf, true);        // quad_perm [2,3,0,1]
+        v = v > o ? v : o;
     }
-    // the fp16 log2 thresholds of the shared scale, after the table
-    float* l2t = reinterpret_cast<float*>(tab + (kMxMagBytes + n + 2 + 15) / 16 * 16);
-    for (int i = threadIdx.x; i < 80; i += kThreads) l2t[i] = i < 40 ? kLog2FloorF16[i] : kLog2RoundF16[i - 40];
-    __syncthreads();
-    const LdsLog2 lt{l2t, l2t + 40};
-    const uint16_t* mags = reinterpret_cast<const uint16_t*>(tab);
-    const uint8_t* lvls = tab + kMxMagBytes;   // lvls[k + 1] for u with fp16 bits lo_bits + k
+    return v;
+}
 
-    const int li = (int)(threadIdx.x & (LPB - 1));
-    const int64_t ntiles = (nb + blocks_per_wg - 1) / blocks_per_wg;
+// float through a DPP move (quad_perm patterns below)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+
+// Persistent 512-thread workgroups; each wave takes 1024-element tiles (the lane
+// mapping above).  BLK: block size 16 or 32.  n_elems is a multiple of BLK.
+template <int M, int BLK>
+__global__ __launch_bounds__(kMxThreads) void mx_fast_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+                                                             uint16_t* __restrict__ scales,
+                                                             uint8_t* __restrict__ codes, int64_t n_elems, int slot,
+                                                             int n, uint32_t lo_m1, MxParams p) {
+    constexpr int LPB = BLK / 8;   // lanes of a block within a half
     typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
     typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
+    extern __shared__ __attribute__((aligned(16))) uint32_t tab[];
+    const int lane = (int)(threadIdx.x & 63);
+    const int wave = (int)(threadIdx.x >> 6);
+    const int q = lane & 3;   // lane within its quad
+    const bool lead = (lane & (LPB - 1)) == 0;
+    const int64_t ntiles = (n_elems + 1023) / 1024;
+    const int64_t stride = (int64_t)gridDim.x * (kMxThreads / 64);
 
-    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-        const int64_t gb = tile * blocks_per_wg + (threadIdx.x / LPB);
-        const bool valid = gb < nb;
-        const int64_t off = (valid ? gb : 0) * (int64_t)block + (int64_t)li * kV;
-        uint32_t w[8];
-        if (valid) {
-            const u32x4_t* q = reinterpret_cast<const u32x4_t*>(x + off);
-            const u32x4_t a = __builtin_nontemporal_load(q), b = __builtin_nontemporal_load(q + 1);
-            w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+    uint32_t w[2][4];
+    auto load = [&](int64_t tile) __attribute__((always_inline)) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int64_t off = tile * 1024 + 512 * h + 8 * lane;
+            if (tile < ntiles && off < n_elems) {   // whole 8-element chunks: n_elems % 16 == 0
+                const u32x4_t a = *reinterpret_cast<const u32x4_t*>(x + off);
+                w[h][0] = a.x; w[h][1] = a.y; w[h][2] = a.z; w[h][3] = a.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) w[h][i] = 0u;
+            }
+        }
+    };
+    // the first tile's loads go out before the table copy, so their latency overlaps it
+    int64_t tile = (int64_t)blockIdx.x * (kMxThreads / 64) + wave;
+    load(tile);
+    {   // copy the table in 16-byte pieces (the slot arrays are 16-byte aligned rows)
+        const uint4* src = reinterpret_cast<const uint4*>(g_mx_tab[slot]);
+        uint4* dst = reinterpret_cast<uint4*>(tab);
+        for (int i = threadIdx.x; i < (n + 2 + 3) / 4; i += kMxThreads) dst[i] = src[i];
+    }
+    // the fp16 log2 thresholds of the shared scale, after the table
+    float* l2t = reinterpret_cast<float*>(tab + (n + 2 + 3) / 4 * 4);
+    for (int i = threadIdx.x; i < 80; i += kMxThreads) l2t[i] = i < 40 ? kLog2FloorF16[i] : kLog2RoundF16[i - 40];
+    __syncthreads();
+    const LdsLog2 lt{l2t, l2t + 40};
+
+    for (; tile < ntiles; tile += stride) {
+        int64_t off[2];
+        bool valid[2];
+        uint32_t m2[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            off[h] = tile * 1024 + 512 * h + 8 * lane;
+            valid[h] = off[h] < n_elems;
+            // block max of |x| over the 16-bit patterns (NaN patterns sort above inf)
+            u16x2_t mp = __builtin_bit_cast(u16x2_t, w[h][0] & 0x7fff7fffu);
+#pragma unroll
+            for (int i = 1; i < 4; ++i)
+                mp = __builtin_elementwise_max(mp, __builtin_bit_cast(u16x2_t, w[h][i] & 0x7fff7fffu));
+            m2[h] = lanes_max<LPB>(mp.x > mp.y ? (uint32_t)mp.x : (uint32_t)mp.y);
+        }
+        // one shared-scale evaluation per lane: a quad holds 4 blocks (block 16: 2 per
+        // half) or 2 (block 32: 1 per half); lane q scales block (half q >> 1, pair q & 1),
+        // then every lane takes the scales of its two blocks from the lanes that made them
+        float sm;
+        if constexpr (BLK == 16) {
+            const float a = dpp_f<0x88>(__builtin_bit_cast(float, m2[0]));   // quad_perm [0,2,0,2]
+            const float b = dpp_f<0x88>(__builtin_bit_cast(float, m2[1]));
+            sm = (q >> 1) ? b : a;
+        } else {
+            sm = (q >> 1) ? __builtin_bit_cast(float, m2[1]) : __builtin_bit_cast(float, m2[0]);
+        }
+        const float s_own = mx_shared_scale<F16>(F16::load((uint16_t)__builtin_bit_cast(uint32_t, sm)), p, lt);
+        const float rs_own = 1.0f / s_own;
+        float s[2], rs[2];
+        if constexpr (BLK == 16) {
+            s[0] = dpp_f<0x50>(s_own);   // quad_perm [0,0,1,1]
+            s[1] = dpp_f<0xFA>(s_own);   // quad_perm [2,2,3,3]
+            rs[0] = dpp_f<0x50>(rs_own);
+            rs[1] = dpp_f<0xFA>(rs_own);
+        } else {
+            s[0] = dpp_f<0x00>(s_own);   // quad_perm [0,0,0,0]
+            s[1] = dpp_f<0xAA>(s_own);   // quad_perm [2,2,2,2]
+            rs[0] = dpp_f<0x00>(rs_own);
+            rs[1] = dpp_f<0xAA>(rs_own);
+        }
+        const bool special = (m2[0] > 0x7c00u) | (m2[1] > 0x7c00u) | !(s_own > 0.f && s_own < __builtin_inff());
+
+        uint32_t y2[2][4];
+        uint32_t cout[2][8];
+        if (__builtin_expect(__builtin_amdgcn_ballot_w64(special) != 0, 0)) {
+            // a NaN in the wave's tile, or a scale that rounds to 0 or inf in fp16 (an
+            // 8-bit scale exponent): the generic element path
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float o[2];
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const float v = F16::load((uint16_t)(e ? w[h][i] >> 16 : w[h][i] & 0xffffu));
+                        const float yv = p.pot ? F16::round(v * rs[h]) : div_T<F16>(v, s[h], rs[h]);
+                        o[e] = F16::round(elem_quant<F16, M>(yv, cout[h][2 * i + e], p.fused) * s[h]);
+                    }
+                    y2[h][i] = (uint32_t)F16::store(o[0]) | ((uint32_t)F16::store(o[1]) << 16);
+                }
         } else {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) w[i] = 0u;
-        }
-        // block max of |x| over the 16-bit patterns (NaN patterns sort above inf)
-        u16x2_t mp = __builtin_bit_cast(u16x2_t, w[0] & 0x7fff7fffu);
+            for (int h = 0; h < 2; ++h) {
+                // u = R16(|x| / s) of each element, packed in pairs like x: for a power-of-two
+                // scale the product is exact; for an FP scale R16(|x| * R32(1/s)) (one
+                // rounding) equals R16(|x| / s) unless the quotient is below 2^-14
+                uint32_t u2[4];
 #pragma unroll
-        for (int i = 1; i < 8; ++i) mp = __builtin_elementwise_max(mp, __builtin_bit_cast(u16x2_t, w[i] & 0x7fff7fffu));
-        uint32_t m2 = mp.x > mp.y ? (uint32_t)mp.x : (uint32_t)mp.y;
-        if constexpr (LPB == 2) {
-            const uint32_t o = (uint32_t)__builtin_amdgcn_mov_dpp((int)m2, 0xB1, 0xf, 0xf, true);   // quad_perm [1,0,3,2]
-            m2 = m2 > o ? m2 : o;
-        }
-        const float amax = F16::load((uint16_t)m2);
-        const float s = mx_shared_scale<F16>(amax, p, lt);
-        const float rs = 1.0f / s;
-
-        uint32_t y2[8];
-        uint32_t cout[kV];
-        if (__builtin_expect((m2 > 0x7c00u) | !(s > 0.f && s < __builtin_inff()), 0)) {
-            // a NaN in the block, or a scale that rounds to 0 or inf in fp16 (an 8-bit
-            // scale exponent): the generic element path
-            float out[kV];
+                for (int i = 0; i < 4; ++i) {
+                    u2[i] = mix_lo(w[h][i], rs[h]);
+                    mix_hi(u2[i], w[h][i], rs[h]);
+                }
+                if (!p.pot) {
+                    u16x2_t mn = __builtin_bit_cast(u16x2_t, u2[0]);
 #pragma unroll
-            for (int i = 0; i < kV; ++i) {
-                const float v = F16::load((uint16_t)(i & 1 ? w[i / 2] >> 16 : w[i / 2] & 0xffffu));
-                const float yv = p.pot ? F16::round(v * rs) : div_T<F16>(v, s, rs);
-                const float q = elem_quant<F16, M>(yv, cout[i], p.fused);
-                out[i] = F16::round(q * s);
-            }
+                    for (int i = 1; i < 4; ++i) mn = __builtin_elementwise_min(mn, __builtin_bit_cast(u16x2_t, u2[i]));
+                    if ((mn.x <= 0x0400u) | (mn.y <= 0x0400u)) {   // near or in the subnormal range: divide
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                y2[i] = (uint32_t)F16::store(out[2 * i]) | ((uint32_t)F16::store(out[2 * i + 1]) << 16);
-        } else {
-            // u = R16(|x| / s) of each element, packed in pairs like x: for a power-of-two
-            // scale the product is exact; for an FP scale R16(|x| * R32(1/s)) (one
-            // rounding) equals R16(|x| / s) unless the quotient is below 2^-14
-            uint32_t u2[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                u2[i] = mix_lo(w[i], rs);
-                mix_hi(u2[i], w[i], rs);
-            }
-            if (!p.pot) {
-                u16x2_t mn = __builtin_bit_cast(u16x2_t, u2[0]);
-#pragma unroll
-                for (int i = 1; i < 8; ++i) mn = __builtin_elementwise_min(mn, __builtin_bit_cast(u16x2_t, u2[i]));
-                if ((mn.x <= 0x0400u) | (mn.y <= 0x0400u)) {   // near or in the subnormal range: divide
-#pragma unroll
-                    for (int i = 0; i < kV; ++i) {
-                        const uint32_t key = i & 1 ? u2[i / 2] >> 16 : u2[i / 2] & 0xffffu;
-                        if (key <= 0x0400u) {
-                            const float a = fabsf(F16::load((uint16_t)(i & 1 ? w[i / 2] >> 16 : w[i / 2] & 0xffffu)));
-                            const uint32_t k2 = F16::store(a / s);
-                            u2[i / 2] = i & 1 ? (u2[i / 2] & 0xffffu) | (k2 << 16) : (u2[i / 2] & 0xffff0000u) | k2;
+                        for (int i = 0; i < 8; ++i) {
+                            const uint32_t key = i & 1 ? u2[i / 2] >> 16 : u2[i / 2] & 0xffffu;
+                            if (key <= 0x0400u) {
+                                const float a =
+                                    fabsf(F16::load((uint16_t)(i & 1 ? w[h][i / 2] >> 16 : w[h][i / 2] & 0xffffu)));
+                                const uint32_t k2 = F16::store(a / s[h]);
+                                u2[i / 2] = i & 1 ? (u2[i / 2] & 0xffffu) | (k2 << 16) : (u2[i / 2] & 0xffff0000u) | k2;
+                            }
                         }
                     }
                 }
-            }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                uint32_t lv[2];
-                u16x2_t q2;
+                for (int i = 0; i < 4; ++i) {
+                    uint32_t e2[2];
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const int key = (int)(h ? u2[i] >> 16 : u2[i] & 0xffffu);
-                    int k;   // word index k + 1 clamped to [0, n + 1] in one v_med3_i32
-                    asm("v_med3_i32 %0, %1, 0, %2" : "=v"(k) : "v"(key - (int)lo_m1), "s"(n + 1));
-                    lv[h] = lvls[k];
-                    q2[h] = mags[lv[h]];
+                    for (int e = 0; e < 2; ++e) {
+                        const int key = (int)(e ? u2[i] >> 16 : u2[i] & 0xffffu);
+                        int k;   // word index k + 1 clamped to [0, n + 1] in one v_med3_i32
+                        asm("v_med3_i32 %0, %1, 0, %2" : "=v"(k) : "v"(key - (int)lo_m1), "s"(n + 1));
+                        e2[e] = tab[k];
+                    }
+                    // the two magnitudes (high halves of the words) as one packed pair
+                    const uint32_t q2 = __builtin_amdgcn_perm(e2[1], e2[0], 0x07060302u);
+                    uint32_t o2 = mix_lo(q2, s[h]);   // R16(q * s): exact product
+                    mix_hi(o2, q2, s[h]);
+                    // the sign of x unless u is +-0 (the reference's u == 0 gives +0 and code 0):
+                    // bit 15 of each half of u2 + 0x7fff7fff is set iff that half is nonzero
+                    // (u <= 0x7c00, so no carry crosses the halves)
+                    const uint32_t sg = w[h][i] & (u2[i] + 0x7fff7fffu) & 0x80008000u;
+                    y2[h][i] = o2 | sg;
+                    cout[h][2 * i] = (e2[0] & 0xffu) | (((sg >> 15) & 1u) << (M + 2));
+                    cout[h][2 * i + 1] = (e2[1] & 0xffu) | ((sg >> 31) << (M + 2));
                 }
-                uint32_t o2 = mix_lo(__builtin_bit_cast(uint32_t, q2), s);   // R16(q * s): exact product
-                mix_hi(o2, __builtin_bit_cast(uint32_t, q2), s);
-                // the sign of x unless u is +-0 (the reference's u == 0 gives +0 and code 0):
-                // bit 15 of each half of u2 + 0x7fff7fff is set iff that half is nonzero
-                // (u <= 0x7c00, so no carry crosses the halves)
-                const uint32_t sg = w[i] & (u2[i] + 0x7fff7fffu) & 0x80008000u;
-                y2[i] = o2 | sg;
-                cout[2 * i] = lv[0] | (((sg >> 15) & 1u) << (M + 2));
-                cout[2 * i + 1] = lv[1] | ((sg >> 31) << (M + 2));
             }
         }
-        if (valid) {
-            u32x4_t* yq = reinterpret_cast<u32x4_t*>(y + off);
-            __builtin_nontemporal_store((u32x4_t){y2[0], y2[1], y2[2], y2[3]}, yq);
-            __builtin_nontemporal_store((u32x4_t){y2[4], y2[5], y2[6], y2[7]}, yq + 1);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if (!valid[h]) continue;
+            *reinterpret_cast<u32x4_t*>(y + off[h]) = (u32x4_t){y2[h][0], y2[h][1], y2[h][2], y2[h][3]};
             if (codes) {
                 if constexpr (M == 1) {
-                    uint32_t w0 = 0, w1 = 0;
+                    uint32_t c = 0;
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        w0 |= (cout[i] & 0xfu) << (4 * i);
-                        w1 |= (cout[8 + i] & 0xfu) << (4 * i);
-                    }
-                    *reinterpret_cast<uint2*>(codes + off / 2) = make_uint2(w0, w1);
+                    for (int i = 0; i < 8; ++i) c |= (cout[h][i] & 0xfu) << (4 * i);
+                    *reinterpret_cast<uint32_t*>(codes + off[h] / 2) = c;
                 } else {
-                    uint32_t cw[4];
+                    uint32_t c0 = 0, c1 = 0;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        cw[i] = (cout[4 * i] & 0xffu) | ((cout[4 * i + 1] & 0xffu) << 8) |
-                                ((cout[4 * i + 2] & 0xffu) << 16) | ((cout[4 * i + 3] & 0xffu) << 24);
-                    *reinterpret_cast<uint4*>(codes + off) = make_uint4(cw[0], cw[1], cw[2], cw[3]);
+                    for (int i = 0; i < 4; ++i) {
+                        c0 |= (cout[h][i] & 0xffu) << (8 * i);
+                        c1 |= (cout[h][4 + i] & 0xffu) << (8 * i);
+                    }
+                    *reinterpret_cast<uint2*>(codes + off[h]) = make_uint2(c0, c1);
                 }
             }
-            if (scales != nullptr && li == 0) scales[gb] = F16::store(s);
+            if (scales != nullptr && lead) scales[off[h] / BLK] = F16::store(s[h]);
         }
+        load(tile + stride);
     }
 }
 
@@ -259,29 +325,31 @@ int build_mx_slot(int slot, int n, uint32_t lo_bits, int fused, hipStream_t st) 
     return status > bad ? status : bad;
 }
 
-template <int M, int LPB>
-int launch_mx_fast(const void* x, void* y, void* scales, void* codes, int64_t nb, int slot, int n, uint32_t lo_bits,
-                   const MxParams& p, int dev, hipStream_t st) {
-    const size_t lds = (size_t)((kMxMagBytes + n + 2 + 15) / 16) * 16 + 80 * sizeof(float);
-    auto kern = mx_fast_kernel<M, LPB>;
+template <int M, int BLK>
+int launch_mx_fast(const void* x, void* y, void* scales, void* codes, int64_t n_elems, int slot, int n,
+                   uint32_t lo_bits, const MxParams& p, int dev, hipStream_t st) {
+    const size_t lds = (size_t)((n + 2 + 3) / 4) * 16 + 80 * sizeof(float);
+    auto kern = mx_fast_kernel<M, BLK>;
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kThreads, lds) != hipSuccess || per_cu <= 0)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kMxThreads, lds) != hipSuccess || per_cu <= 0)
         return 0;
-    const int64_t blocks_per_wg = kThreads / LPB;
-    const int64_t ntiles = (nb + blocks_per_wg - 1) / blocks_per_wg;
-    const int64_t resident = (int64_t)g_mx_cus[dev] * per_cu;
-    const int64_t rounds = (ntiles + resident - 1) / resident;
-    const int64_t grid = (ntiles + rounds - 1) / rounds;
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), lds, st, (const uint16_t*)x, (uint16_t*)y,
-                       (uint16_t*)scales, (uint8_t*)codes, nb, slot, n, lo_bits - 1u, p);
+    const int64_t ntiles = (n_elems + 1023) / 1024;
+    const int64_t waves_needed = ntiles;
+    const int64_t resident = (int64_t)g_mx_cus[dev] * per_cu * (kMxThreads / 64);
+    // as many rounds as the resident waves need, with the tiles spread evenly over them
+    const int64_t rounds = (waves_needed + resident - 1) / resident;
+    const int64_t waves = (waves_needed + rounds - 1) / rounds;
+    const int64_t grid = (waves + kMxThreads / 64 - 1) / (kMxThreads / 64);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kMxThreads), lds, st, (const uint16_t*)x, (uint16_t*)y,
+                       (uint16_t*)scales, (uint8_t*)codes, n_elems, slot, n, lo_bits - 1u, p);
     return 1;
 }
 
 template <int M>
-int mx_fast_block(int block, const void* x, void* y, void* scales, void* codes, int64_t nb, int slot, int n,
+int mx_fast_block(int block, const void* x, void* y, void* scales, void* codes, int64_t n_elems, int slot, int n,
                   uint32_t lo_bits, const MxParams& p, int dev, hipStream_t st) {
-    if (block == 16) return launch_mx_fast<M, 1>(x, y, scales, codes, nb, slot, n, lo_bits, p, dev, st);
-    return launch_mx_fast<M, 2>(x, y, scales, codes, nb, slot, n, lo_bits, p, dev, st);
+    if (block == 16) return launch_mx_fast<M, 16>(x, y, scales, codes, n_elems, slot, n, lo_bits, p, dev, st);
+    return launch_mx_fast<M, 32>(x, y, scales, codes, n_elems, slot, n, lo_bits, p, dev, st);
 }
 
 }  // namespace
@@ -322,12 +390,12 @@ int hbq_mx_fast_try(const void* x, void* y, void* scales, void* codes, int64_t r
             if (rc != 0) return 0;
         }
     }
-    const int64_t nb = rows * (cols / block);
-    if (nb == 0) return 1;
+    const int64_t n_elems = rows * cols;
+    if (n_elems == 0) return 1;
     switch (mbit) {
-        case 1: return mx_fast_block<1>(block, x, y, scales, codes, nb, slot, n, lo_bits, p, dev, st);
-        case 2: return mx_fast_block<2>(block, x, y, scales, codes, nb, slot, n, lo_bits, p, dev, st);
-        case 3: return mx_fast_block<3>(block, x, y, scales, codes, nb, slot, n, lo_bits, p, dev, st);
-        default: return mx_fast_block<5>(block, x, y, scales, codes, nb, slot, n, lo_bits, p, dev, st);
+        case 1: return mx_fast_block<1>(block, x, y, scales, codes, n_elems, slot, n, lo_bits, p, dev, st);
+        case 2: return mx_fast_block<2>(block, x, y, scales, codes, n_elems, slot, n, lo_bits, p, dev, st);
+        case 3: return mx_fast_block<3>(block, x, y, scales, codes, n_elems, slot, n, lo_bits, p, dev, st);
+        default: return mx_fast_block<5>(block, x, y, scales, codes, n_elems, slot, n, lo_bits, p, dev, st);
     }
 }

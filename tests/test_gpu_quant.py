@@ -321,6 +321,21 @@ def test_mxfp_table_kernel_equals_generic(gpu, name, dyn):
     assert mismatches(to_bits(fast.scales), to_bits(gen.scales), "f16") == 0
 
 
+@pytest.mark.parametrize("name", ["mxfp4", "mxfp8", "nvfp4"])
+@pytest.mark.parametrize("shape", [(1, 32), (3, 96), (7, 208), (5, 1056), (33, 4064)])
+def test_mxfp_table_kernel_partial_tiles(gpu, oracle, name, shape):
+    """Shapes whose element count is not a multiple of a wave's 1024-element tile: the table
+    kernel's partial last tile against the oracle."""
+    rows, cols = shape
+    if cols % MXCFG[name]["block_size"]:
+        pytest.skip("ragged rows take the generic kernel")
+    x = synth(rows, cols, 19, "f16", outliers=min(8, cols))
+    out = _mx(MXCFG[name]).quantize(x.to(gpu))
+    y, s = oracle.mxfp_qdq(to_bits(x), "f16", **MXCFG[name])
+    assert mismatches(to_bits(out.y), y, "f16") == 0
+    assert mismatches(to_bits(out.scales), s, "f16") == 0
+
+
 @pytest.mark.parametrize("name", ["hbq_a_act", "hbq_a_wgt", "hbq_kv4"])
 def test_hbq_causal_zero_blocks(gpu, oracle, name):
     """Attention-weight-like input (row i zero past column i): waves whose eight blocks are all
