@@ -279,7 +279,7 @@ def prefill_extra(dev, T=2048, iters=3):
     Then the same with the decoder weights packed (hbq_amd.packed), checked for the same logits."""
     from hbq_amd.llama import LlamaConfig, LlamaForCausalLM
     from hbq_amd.module import _QBaseLinear
-    from hbq_amd.ops import stack_qkv_gemms, use_hip_fp32_gemm
+    from hbq_amd.ops import fuse_input_quantizers, stack_qkv_gemms, use_hip_fp32_gemm
     from hbq_amd.packed import pack_linear_weights
     from hbq_amd.ptq import PTQ
     cfg = LlamaConfig()
@@ -303,8 +303,21 @@ def prefill_extra(dev, T=2048, iters=3):
         for _ in range(iters):
             out = m(ids)
         torch.cuda.synchronize()
-    t = (time.perf_counter() - t0) / iters
+    t_sep = (time.perf_counter() - t0) / iters
     assert torch.isfinite(out).all()
+    # the linears' input quantizers computed inside the norms and the SiLU product (one pass
+    # fewer over X for q/k/v, gate/up and down): same logits; the timed configuration
+    fuse_input_quantizers(m)
+    with torch.no_grad():
+        m(ids)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            out_f = m(ids)
+        torch.cuda.synchronize()
+    t = (time.perf_counter() - t0) / iters
+    same_f = bool(torch.equal(out.view(torch.int16), out_f.view(torch.int16)))
+    del out_f
     w_bytes = sum(mod.weight.numel() * 2 for mod in m.modules() if isinstance(mod, _QBaseLinear) and mod is not m.lm_head)
     del m
     torch.cuda.empty_cache()
@@ -317,6 +330,7 @@ def prefill_extra(dev, T=2048, iters=3):
     p.inject_quantizers()
     use_hip_fp32_gemm(m)
     stack_qkv_gemms(m)
+    fuse_input_quantizers(m)
     pack_linear_weights(m)
     pw_bytes = sum(mod.packed_weight.nbytes for mod in m.modules() if "packed_weight" in mod.__dict__)
     with torch.no_grad():
@@ -332,6 +346,8 @@ def prefill_extra(dev, T=2048, iters=3):
     torch.cuda.empty_cache()
     return {"cfg4_prefill_ms": round(t * 1e3, 2), "cfg4_prefill_tokens_per_s": round(T / t, 1),
             "cfg4_weight_quant_ms": round(t_wq * 1e3, 1),
+            "cfg4_prefill_separate_input_quant_ms": round(t_sep * 1e3, 2),
+            "cfg4_fused_input_quant_logits_identical": same_f,
             "cfg4_prefill_packed_ms": round(t_p * 1e3, 2), "cfg4_packed_logits_identical": same,
             "cfg4_decoder_weight_GB_fp16": round(w_bytes / 1e9, 2),
             "cfg4_decoder_weight_GB_packed": round(pw_bytes / 1e9, 2)}

@@ -42,6 +42,8 @@ SIGNATURES = {
     "hbq_rms_prep": ([_P, _P, _P, _P, _I64, _I, _P], _I),
     "hbq_rms_apply": ([_P, _P, _P, _P, _I64, _I64, _I, _P], _I),
     "hbq_silu_mul": ([_P, _P, _P, _I64, _I, _P], _I),
+    "hbq_rms_apply_hbq_qdq": ([_P, _P, _P, _P, _I64, _I64] + [_I] * 12 + [_P], _I),
+    "hbq_silu_mul_hbq_qdq": ([_P, _P, _P, _I64, _I64] + [_I] * 12 + [_P], _I),
     "hbq_rope": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P], _I),
     "hbq_hbq_packed_strides": ([_I64, _I, _I, _I, _I, _I, _P], _I),
     "hbq_hbq_pack": ([_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _I, _P], _I),

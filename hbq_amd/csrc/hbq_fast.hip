@@ -26,6 +26,7 @@
 
 #include "hbq_capi_internal.h"
 #include "hbq_fast.h"
+#include "model_math.h"
 #include "quant_common.h"
 
 namespace hbq {
@@ -152,14 +153,14 @@ constexpr int fast_threads() { return T::dt == kF16 ? 512 : 256; }
 // Block 128 (8 lanes x 16 elements).  Per-wave magnitude tables, laid out
 // [scheme][candidate][block-in-wave][level] with rows padded by one entry so
 // that the eight blocks of a wave fall on different LDS banks.
-template <class T, int M, int L2B, int S>
+template <class T, int M, int L2B, int S, int SRC = kSrcX>
 __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typename T::storage* __restrict__ x,
                                                             typename T::storage* __restrict__ y,
                                                             typename T::storage* __restrict__ l1_out,
                                                             uint8_t* __restrict__ l2i_out,
                                                             uint8_t* __restrict__ sch_out,
                                                             uint8_t* __restrict__ codes, int64_t nb, int64_t causal_t,
-                                                            int slot, FastParams p) {
+                                                            int slot, FastParams p, FastSrc src, int64_t cols) {
     using DT = DTabT<T>;
     constexpr int lpb = 8;
     constexpr int bpw = 64 / lpb;
@@ -232,9 +233,32 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
         uint32_t w[8];
         if (valid) {
             typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-            const u32x4_t* q = reinterpret_cast<const u32x4_t*>(x + off);
-            const u32x4_t a = __builtin_nontemporal_load(q), b = __builtin_nontemporal_load(q + 1);
-            w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+            if constexpr (SRC == kSrcX) {
+                const u32x4_t* q = reinterpret_cast<const u32x4_t*>(x + off);
+                const u32x4_t a = __builtin_nontemporal_load(q), b = __builtin_nontemporal_load(q + 1);
+                w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+            } else {
+                // the producing pass's 16 outputs, computed here instead of read back
+                const u32x4_t* qa = reinterpret_cast<const u32x4_t*>(src.a + off);
+                const u32x4_t a0 = __builtin_nontemporal_load(qa), a1 = __builtin_nontemporal_load(qa + 1);
+                const int64_t row = off / cols;
+                const u32x4_t* qb = reinterpret_cast<const u32x4_t*>(src.b + (SRC == kSrcRms ? off - row * cols : off));
+                const u32x4_t b0 = qb[0], b1 = qb[1];
+                const uint32_t aw[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+                const uint32_t bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+                const float r = SRC == kSrcRms ? src.rs[row] : 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    uint32_t o[2];
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const float av = T::load((typename T::storage)(aw[i] >> (16 * h)));
+                        const float bv = T::load((typename T::storage)(bw[i] >> (16 * h)));
+                        o[h] = store_t<T>(SRC == kSrcRms ? rms_apply_one<T>(av, r, bv) : silu_mul_one<T>(av, bv));
+                    }
+                    w[i] = o[0] | (o[1] << 16);
+                }
+            }
         } else {
 #pragma unroll
             for (int i = 0; i < 8; ++i) w[i] = 0u;
@@ -514,16 +538,16 @@ int build_slot(int slot, const FastParams& p, hipStream_t st) {
     return status;   // 0 ready, > 0 the table shape does not fit this configuration
 }
 
-template <class T, int M, int L2B, int S>
+template <class T, int M, int L2B, int S, int SRC = kSrcX>
 int launch_fast(const void* x, void* y, void* l1, void* l2i, void* sch, void* codes, int64_t nb, int64_t causal_t,
-                int slot, const FastParams& p, int dev, hipStream_t st) {
+                int slot, const FastParams& p, int dev, hipStream_t st, const FastSrc& src = FastSrc{}, int64_t cols = 0) {
     constexpr int lpb_log2 = 3;
     constexpr int NTH = fast_threads<T>();
     using St = typename T::storage;
     const size_t lds = (size_t)S * (p.n + 2) * 4 +
                        (size_t)(NTH >> lpb_log2) * S * kFastJ * ((1 << (M + 2)) + 1) * sizeof(DTabT<T>);
     if (lds > 160 * 1024) return 0;
-    auto kern = hbq_fast_kernel<T, M, L2B, S>;
+    auto kern = hbq_fast_kernel<T, M, L2B, S, SRC>;
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, NTH, lds) != hipSuccess || per_cu <= 0)
         return 0;
@@ -539,7 +563,7 @@ int launch_fast(const void* x, void* y, void* l1, void* l2i, void* sch, void* co
     const int64_t rounds = (ntiles + resident - 1) / resident;
     const int64_t grid = (ntiles + rounds - 1) / rounds;
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NTH), lds, st, (const St*)x, (St*)y, (St*)l1,
-                       (uint8_t*)l2i, (uint8_t*)sch, (uint8_t*)codes, nb, causal_t, slot, p);
+                       (uint8_t*)l2i, (uint8_t*)sch, (uint8_t*)codes, nb, causal_t, slot, p, src, cols);
     return 1;
 }
 
@@ -560,16 +584,14 @@ int fast_by_shape(int l2b, int S, const void* x, void* y, void* l1, void* l2i, v
 
 using namespace hbq;
 
-int hbq_fast_try(const void* x, void* y, void* l1, void* l2i, void* sch, void* codes, int64_t rows, int64_t cols,
-                 int dtype, int block, int mbit, int l2b, int l2_sc_bit, int scheme, const HbqParams& hp,
-                 hipStream_t st, int64_t causal_t) {
+// Configuration checks, kernel parameters and the per-device level table of the table
+// kernel: 1 ready (p, slot, dev set), 0 not for this kernel, < 0 a HIP error.
+static int fast_setup(FastParams& p, int& slot, int& dev, int dtype, int block, int mbit, int l2b, int l2_sc_bit,
+                      int scheme, const HbqParams& hp, hipStream_t st) {
     if (dtype != kF16 && dtype != kBF16) return 0;
     if (mbit < 1 || mbit > 3 || hp.J > kFastJ) return 0;
     if (l2b != 8 && l2b != 16 && l2b != 32) return 0;
-    int lb = 0;
-    while ((1 << lb) < block) ++lb;
     if (block != 128 || block % l2b) return 0;
-    if (cols % block || ((uintptr_t)x % 16) || ((uintptr_t)y % 16) || (codes && ((uintptr_t)codes % 16))) return 0;
     const int S = scheme == 7 ? 2 : 1;
 
     // table range [2^lo, 2^hi): below 2^-(m+2) every candidate rounds to level 0 (l2 >= 1);
@@ -581,7 +603,7 @@ int hbq_fast_try(const void* x, void* y, void* l1, void* l2i, void* sch, void* c
     while ((float)(1 << (hi - 3)) < l2max) ++hi;
     const int lo = -(mbit + 2);
     if (hi - lo > kLutMaxBinades) return 0;
-    FastParams p{};
+    p = FastParams{};
     p.S = S;
     p.J = hp.J;
     p.L = 1 << (mbit + 2);
@@ -600,43 +622,55 @@ int hbq_fast_try(const void* x, void* y, void* l1, void* l2i, void* sch, void* c
     // the kernel quantizes the L1 scale to E5M3 without subnormals
     if (hp.sf.allow_sub || hp.sf.emax != 15.f || hp.sf.mshift != 8.f || hp.sf.emin != -14.f) return 0;
 
-    int dev = 0;
+    dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
-    int slot = -1;
-    {
-        std::lock_guard<std::mutex> g(g_mu);
-        if (g_cus[dev] == 0) {
-            int cus = 0;
-            if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-                return 0;
-            g_cus[dev] = cus;
-        }
-        const LutKey key{dtype, mbit, scheme, l2_sc_bit, hp.fused};
-        for (int i = 0; i < kLutSlots; ++i)
-            if (g_state[dev][i] != 0 && g_keys[dev][i] == key) slot = i;
-        if (slot >= 0 && g_state[dev][slot] < 0) return 0;
-        if (slot < 0) {
-            slot = g_next[dev];
-            g_next[dev] = (g_next[dev] + 1) % kLutSlots;
-            g_keys[dev][slot] = key;
-            int rc;
-            if (dtype == kF16)
-                rc = mbit == 1 ? build_slot<F16, 1>(slot, p, st) : mbit == 2 ? build_slot<F16, 2>(slot, p, st)
-                                                                               : build_slot<F16, 3>(slot, p, st);
-            else
-                rc = mbit == 1 ? build_slot<BF16, 1>(slot, p, st) : mbit == 2 ? build_slot<BF16, 2>(slot, p, st)
-                                                                                : build_slot<BF16, 3>(slot, p, st);
-            if (rc < 0 || rc == HBQ_ERR_HIP) {
-                g_state[dev][slot] = 0;
-                return -HBQ_ERR_HIP;
-            }
-            g_state[dev][slot] = rc == 0 ? 1 : -1;
-            if (rc != 0) return 0;
-        }
+    slot = -1;
+    std::lock_guard<std::mutex> g(g_mu);
+    if (g_cus[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            return 0;
+        g_cus[dev] = cus;
     }
+    const LutKey key{dtype, mbit, scheme, l2_sc_bit, hp.fused};
+    for (int i = 0; i < kLutSlots; ++i)
+        if (g_state[dev][i] != 0 && g_keys[dev][i] == key) slot = i;
+    if (slot >= 0 && g_state[dev][slot] < 0) return 0;
+    if (slot < 0) {
+        slot = g_next[dev];
+        g_next[dev] = (g_next[dev] + 1) % kLutSlots;
+        g_keys[dev][slot] = key;
+        int rc;
+        if (dtype == kF16)
+            rc = mbit == 1 ? build_slot<F16, 1>(slot, p, st) : mbit == 2 ? build_slot<F16, 2>(slot, p, st)
+                                                                           : build_slot<F16, 3>(slot, p, st);
+        else
+            rc = mbit == 1 ? build_slot<BF16, 1>(slot, p, st) : mbit == 2 ? build_slot<BF16, 2>(slot, p, st)
+                                                                            : build_slot<BF16, 3>(slot, p, st);
+        if (rc < 0 || rc == HBQ_ERR_HIP) {
+            g_state[dev][slot] = 0;
+            return -HBQ_ERR_HIP;
+        }
+        g_state[dev][slot] = rc == 0 ? 1 : -1;
+        if (rc != 0) return 0;
+    }
+    return 1;
+}
+
+int hbq_fast_try(const void* x, void* y, void* l1, void* l2i, void* sch, void* codes, int64_t rows, int64_t cols,
+                 int dtype, int block, int mbit, int l2b, int l2_sc_bit, int scheme, const HbqParams& hp,
+                 hipStream_t st, int64_t causal_t) {
+    if (block != 128 || cols % block || ((uintptr_t)x % 16) || ((uintptr_t)y % 16) ||
+        (codes && ((uintptr_t)codes % 16)))
+        return 0;
+    FastParams p;
+    int slot = -1, dev = 0;
+    const int rs = fast_setup(p, slot, dev, dtype, block, mbit, l2b, l2_sc_bit, scheme, hp, st);
+    if (rs <= 0) return rs;
+    const int S = p.S;
     const int64_t nb = rows * (cols / block);
     if (nb == 0) return 1;
-    const int lpb_log2 = lb - 4;
+    const int lpb_log2 = 3;
     int done;
 #define FAST_T(TT)                                                                                              \
     (mbit == 1 ? fast_by_shape<TT, 1>(l2b, S, x, y, l1, l2i, sch, codes, cols, block, lpb_log2, nb, causal_t, slot, p, dev, st) \
@@ -645,4 +679,36 @@ int hbq_fast_try(const void* x, void* y, void* l1, void* l2i, void* sch, void* c
     done = dtype == kF16 ? FAST_T(F16) : FAST_T(BF16);
 #undef FAST_T
     return done;
+}
+
+namespace {
+template <class T, int SRC>
+int launch_src(int l2b, void* y, int64_t nb, int slot, const FastParams& p, int dev, hipStream_t st,
+               const FastSrc& src, int64_t cols) {
+    switch (l2b) {
+        case 8: return launch_fast<T, 2, 8, 1, SRC>(nullptr, y, nullptr, nullptr, nullptr, nullptr, nb, 0, slot, p, dev, st, src, cols);
+        case 16: return launch_fast<T, 2, 16, 1, SRC>(nullptr, y, nullptr, nullptr, nullptr, nullptr, nb, 0, slot, p, dev, st, src, cols);
+        case 32: return launch_fast<T, 2, 32, 1, SRC>(nullptr, y, nullptr, nullptr, nullptr, nullptr, nb, 0, slot, p, dev, st, src, cols);
+    }
+    return 0;
+}
+}  // namespace
+
+int hbq_fast_try_src(const FastSrc& src, void* y, int64_t rows, int64_t cols, int dtype, int block, int mbit,
+                     int l2b, int l2_sc_bit, int scheme, const HbqParams& hp, hipStream_t st) {
+    // the activation formats only (E2M2 elements, one scheme): the kernels instantiated here
+    if (mbit != 2 || scheme == 7 || (src.kind != kSrcRms && src.kind != kSrcSilu)) return 0;
+    if (block != 128 || cols % block || ((uintptr_t)y % 16) || ((uintptr_t)src.a % 16) || ((uintptr_t)src.b % 16))
+        return 0;
+    FastParams p;
+    int slot = -1, dev = 0;
+    const int rs = fast_setup(p, slot, dev, dtype, block, mbit, l2b, l2_sc_bit, scheme, hp, st);
+    if (rs <= 0) return rs;
+    const int64_t nb = rows * (cols / block);
+    if (nb == 0) return 1;
+    if (dtype == kF16)
+        return src.kind == kSrcRms ? launch_src<F16, kSrcRms>(l2b, y, nb, slot, p, dev, st, src, cols)
+                                   : launch_src<F16, kSrcSilu>(l2b, y, nb, slot, p, dev, st, src, cols);
+    return src.kind == kSrcRms ? launch_src<BF16, kSrcRms>(l2b, y, nb, slot, p, dev, st, src, cols)
+                               : launch_src<BF16, kSrcSilu>(l2b, y, nb, slot, p, dev, st, src, cols);
 }

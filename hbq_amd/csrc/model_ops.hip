@@ -11,15 +11,11 @@
 #include <initializer_list>
 
 #include "hbq_capi_internal.h"
+#include "model_math.h"
 #include "quant_common.h"
 
 namespace hbq {
 namespace {
-
-template <class T>
-__device__ __forceinline__ uint32_t store_t(float v) {
-    return (T::dt == kBF16 && v != v) ? 0x7FC0u : (uint32_t)T::store(v);
-}
 
 template <class T>
 __device__ __forceinline__ void unpack8(const u32x4& v, float (&x)[8]) {
@@ -75,11 +71,7 @@ __global__ __launch_bounds__(kThreads) void rms_apply_kernel(const uint16_t* __r
     unpack8<T>(*reinterpret_cast<const u32x4*>(x + 8 * u), xv);
     unpack8<T>(*reinterpret_cast<const u32x4*>(w + 8 * c8), wv);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        float h = xv[e] * r;
-        asm("" : "+v"(h));               // the fp32 product is rounded before the conversion
-        o[e] = wv[e] * T::round(h);
-    }
+    for (int e = 0; e < 8; ++e) o[e] = rms_apply_one<T>(xv[e], r, wv[e]);
     *reinterpret_cast<u32x4*>(y + 8 * u) = pack8<T>(o);
 }
 
@@ -94,12 +86,7 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __re
     unpack8<T>(*reinterpret_cast<const u32x4*>(g + 8 * u), gv);
     unpack8<T>(*reinterpret_cast<const u32x4*>(up + 8 * u), uv);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        float d = 1.0f + expf(-gv[e]);
-        asm("" : "+v"(d));
-        const float s = gv[e] / d;
-        o[e] = T::round(s) * uv[e];
-    }
+    for (int e = 0; e < 8; ++e) o[e] = silu_mul_one<T>(gv[e], uv[e]);
     *reinterpret_cast<u32x4*>(y + 8 * u) = pack8<T>(o);
 }
 

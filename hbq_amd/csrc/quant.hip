@@ -621,6 +621,51 @@ int hbq_hbq_qdq_causal(void* x, int64_t mats, int64_t t, int dtype, int block_si
     return hbq_check_launch("hbq_hbq_qdq_causal");
 }
 
+// The HBQ quantizer on the output of the pass that produces it, computed in the
+// quantizer's load step (the producer's output never written).
+static int hbq_src_qdq(const FastSrc& src, void* y, int64_t rows, int64_t cols, int dtype, int block_size, int ebit,
+                       int mbit, int sc_ebit, int sc_mbit, int l2_block_size, int l2_sc_bit, int l2_scheme,
+                       int scale_allow_subnormal, int use_ceil, int compiled, void* stream, const char* name) {
+    hbq_clear_error();
+    if (rows < 0 || cols < 0) return hbq_fail(HBQ_ERR_INVALID, "negative size");
+    if (dtype != kF16 && dtype != kBF16) return hbq_fail(HBQ_ERR_UNSUPPORTED, "%s takes fp16 / bf16", name);
+    if (rows == 0 || cols == 0) return 0;
+    if (!src.a || !src.b || !y || (src.kind == kSrcRms && !src.rs)) return hbq_fail(HBQ_ERR_INVALID, "null pointer");
+    HbqParams p{};
+    int S = 1;
+    Geometry g;
+    if (int rc = hbq_setup(p, S, g, src.a, y, nullptr, rows, cols, dtype, block_size, ebit, mbit, sc_ebit, sc_mbit,
+                           l2_block_size, l2_sc_bit, l2_scheme, scale_allow_subnormal, use_ceil))
+        return rc;
+    p.fused = compiled != 0;
+    if (g.nb == 0) return 0;
+    const int fr = hbq_fast_try_src(src, y, rows, cols, dtype, block_size, mbit, l2_block_size, l2_sc_bit, l2_scheme,
+                                    p, (hipStream_t)stream);
+    if (fr < 0) return -fr;
+    if (fr == 0)
+        return hbq_fail(HBQ_ERR_UNSUPPORTED, "%s: configuration outside the fused kernels (E2M2 elements, one "
+                        "L2 scheme, block 128, 16-byte aligned rows)", name);
+    return hbq_check_launch(name);
+}
+
+int hbq_rms_apply_hbq_qdq(const void* x, const float* rs, const void* w, void* y, int64_t rows, int64_t cols,
+                          int dtype, int block_size, int ebit, int mbit, int sc_ebit, int sc_mbit, int l2_block_size,
+                          int l2_sc_bit, int l2_scheme, int scale_allow_subnormal, int use_ceil, int compiled,
+                          void* stream) {
+    const FastSrc src{kSrcRms, (const uint16_t*)x, (const uint16_t*)w, rs};
+    return hbq_src_qdq(src, y, rows, cols, dtype, block_size, ebit, mbit, sc_ebit, sc_mbit, l2_block_size, l2_sc_bit,
+                       l2_scheme, scale_allow_subnormal, use_ceil, compiled, stream, "hbq_rms_apply_hbq_qdq");
+}
+
+int hbq_silu_mul_hbq_qdq(const void* g, const void* u, void* y, int64_t rows, int64_t cols, int dtype,
+                         int block_size, int ebit, int mbit, int sc_ebit, int sc_mbit, int l2_block_size,
+                         int l2_sc_bit, int l2_scheme, int scale_allow_subnormal, int use_ceil, int compiled,
+                         void* stream) {
+    const FastSrc src{kSrcSilu, (const uint16_t*)g, (const uint16_t*)u, nullptr};
+    return hbq_src_qdq(src, y, rows, cols, dtype, block_size, ebit, mbit, sc_ebit, sc_mbit, l2_block_size, l2_sc_bit,
+                       l2_scheme, scale_allow_subnormal, use_ceil, compiled, stream, "hbq_silu_mul_hbq_qdq");
+}
+
 int hbq_scale_quant(const void* x, void* y, int64_t n, int dtype, int ebit, int mbit, int allow_subnormal,
                     int use_ceil, int clip, void* stream) {
     hbq_clear_error();

@@ -71,6 +71,52 @@ class RMSNorm(nn.Module):
             x = x + res
         return x, self.forward(x)
 
+    def add_norm_quant(self, x, res, aq):
+        """(s, y, True) with y = aq.q(norm(s)) from one HIP pass that never writes the norm's
+        output, for an input quantizer aq that the fused kernels take (fusable_quantizer);
+        else add_norm's (s, y, False)."""
+        if aq is not None and _fused_norm_ok(x, res, self.weight) and x.shape[-1] % 128 == 0:
+            s = torch.empty_like(x) if res is not None else x
+            sq = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+            st = _lib.stream_of(x)
+            _lib.check(_lib.lib().hbq_rms_prep(_lib.ptr(x), _lib.ptr(res), _lib.ptr(s) if res is not None else None,
+                                               _lib.ptr(sq), x.numel(), _lib.DTYPE_CODE[x.dtype], st))
+            rs = torch.rsqrt(sq.mean(-1, keepdim=True) + self.eps)
+            y = torch.empty_like(x)
+            rc = _lib.lib().hbq_rms_apply_hbq_qdq(_lib.ptr(s), _lib.ptr(rs), _lib.ptr(self.weight), _lib.ptr(y),
+                                                  x.numel() // x.shape[-1], x.shape[-1], _lib.DTYPE_CODE[x.dtype],
+                                                  *aq.abi_args(), st)
+            if rc == 0:
+                return s, y, True
+            _unfusable(aq, rc)
+            _lib.check(_lib.lib().hbq_rms_apply(_lib.ptr(s), _lib.ptr(rs), _lib.ptr(self.weight), _lib.ptr(y),
+                                                x.numel() // x.shape[-1], x.shape[-1], _lib.DTYPE_CODE[x.dtype], st))
+            return s, y, False
+        return self.add_norm(x, res) + (False,)
+
+
+def fusable_quantizer(mods):
+    """The input quantizer that the linears mods apply to one shared input, when the fused
+    producer-and-quantizer passes (hbq_rms_apply_hbq_qdq, hbq_silu_mul_hbq_qdq) may
+    compute it: the same HBQQuantizer on every linear, with the class's own q and no
+    statistics kept; else None."""
+    from .quantizer import HBQQuantizer
+    aq = mods[0].aq
+    if (type(aq) is not HBQQuantizer or "q" in aq.__dict__ or aq.keep_l2_scale
+            or aq.__dict__.get("_src_unsupported") or type(mods[0]).forward is not _QBaseLinear.forward):
+        return None
+    for m in mods[1:]:
+        if not same_quantizer(aq, m.aq) or type(m).forward is not _QBaseLinear.forward:
+            return None
+    return aq
+
+
+def _unfusable(aq, rc):
+    """After a fused pass declined aq's configuration: remember it, and raise other errors."""
+    if rc != _lib.ERR_UNSUPPORTED:
+        _lib.check(rc)
+    aq.__dict__["_src_unsupported"] = True
+
 
 def _fused_ok(*ts):
     t0 = ts[0]
@@ -93,6 +139,21 @@ def silu_mul(gate, up):
     _lib.check(_lib.lib().hbq_silu_mul(_lib.ptr(gate), _lib.ptr(up), _lib.ptr(y), gate.numel(),
                                        _lib.DTYPE_CODE[gate.dtype], _lib.stream_of(gate)))
     return y
+
+
+def silu_mul_quant(gate, up, aq):
+    """aq.q(silu(gate) * up) from one HIP pass that never writes the product, for an input
+    quantizer aq of down_proj that the fused kernels take; None otherwise."""
+    if not (_fused_ok(gate, up) and gate.shape == up.shape and gate.shape[-1] % 128 == 0):
+        return None
+    y = torch.empty_like(gate)
+    rc = _lib.lib().hbq_silu_mul_hbq_qdq(_lib.ptr(gate), _lib.ptr(up), _lib.ptr(y), gate.numel() // gate.shape[-1],
+                                         gate.shape[-1], _lib.DTYPE_CODE[gate.dtype], *aq.abi_args(),
+                                         _lib.stream_of(gate))
+    if rc == 0:
+        return y
+    _unfusable(aq, rc)
+    return None
 
 
 def rotary(cfg, T, device):
@@ -246,12 +307,13 @@ class QLlamaAttention(nn.Module):
         out = _batched_gemm(pg, vT) if vT is not None else torch.matmul(pg, v)
         return out.view(b, H, T, d), p
 
-    def forward(self, x, cos, sin):
+    def forward(self, x, cos, sin, quantized=False):
+        """quantized: x is already q_proj.aq's output (the quantizer shared by q, k and v)."""
         b, T, _ = x.shape
         qp, kp, vp = self.q_proj, self.k_proj, self.v_proj
-        if same_quantizer(qp.aq, kp.aq) and same_quantizer(qp.aq, vp.aq):
+        if quantized or (same_quantizer(qp.aq, kp.aq) and same_quantizer(qp.aq, vp.aq)):
             # q, k and v quantize the same input with the same function: quantize it once
-            xq = qp.aq(x)
+            xq = x if quantized else qp.aq(x)
             if self.stack_qkv:
                 q, k, v = forward_quantized_stacked((qp, kp, vp), xq)
             else:
@@ -290,13 +352,21 @@ class QLlamaMLP(nn.Module):
         self.down_proj = _QBaseLinear(cfg.intermediate_size, cfg.hidden_size, bias=False)
         self.quantizer_after_act_fn = None
 
-    def forward(self, x):
-        if same_quantizer(self.gate_proj.aq, self.up_proj.aq):
-            xq = self.gate_proj.aq(x)     # gate and up quantize the same input identically
+    def forward(self, x, quantized=False, fuse_quant=False):
+        """quantized: x is already gate_proj.aq's output (the quantizer shared by gate and up).
+        fuse_quant: down_proj's input quantizer computed with the SiLU product in one pass
+        where the fused kernel takes it."""
+        if quantized or same_quantizer(self.gate_proj.aq, self.up_proj.aq):
+            xq = x if quantized else self.gate_proj.aq(x)   # gate and up quantize the same input identically
             gate, up = self.gate_proj.forward_quantized(xq), self.up_proj.forward_quantized(xq)
         else:
             gate, up = self.gate_proj(x), self.up_proj(x)
         if self.quantizer_after_act_fn is None:
+            aq = fusable_quantizer((self.down_proj,)) if fuse_quant else None
+            if aq is not None:
+                yq = silu_mul_quant(gate, up, aq)
+                if yq is not None:
+                    return self.down_proj.forward_quantized(yq)
             y = silu_mul(gate, up)
             if y is not None:
                 return self.down_proj(y)
@@ -313,13 +383,24 @@ class DecoderLayer(nn.Module):
         self.self_attn = QLlamaAttention(cfg)
         self.post_attention_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
         self.mlp = QLlamaMLP(cfg)
+        # the linears' input quantizers computed by the passes producing their inputs
+        # (the norms and the SiLU product) where the fused kernels take them; same bits
+        self.fuse_input_quant = False
 
     def forward(self, x, cos, sin, res=None):
         """(x, r) with x + r the layer's output, for input x + res: the residual add
         that ends a layer is left to the next norm, which fuses it."""
-        x, h = self.input_layernorm.add_norm(x, res)
-        x, h = self.post_attention_layernorm.add_norm(x, self.self_attn(h, cos, sin))
-        return x, self.mlp(h)
+        attn, mlp = self.self_attn, self.mlp
+        if not self.fuse_input_quant:
+            x, h = self.input_layernorm.add_norm(x, res)
+            x, h = self.post_attention_layernorm.add_norm(x, attn(h, cos, sin))
+            return x, mlp(h)
+        x, h, hq = self.input_layernorm.add_norm_quant(x, res, fusable_quantizer((attn.q_proj, attn.k_proj,
+                                                                                  attn.v_proj)))
+        a = attn(h, cos, sin, quantized=hq)
+        x, h, hq = self.post_attention_layernorm.add_norm_quant(x, a, fusable_quantizer((mlp.gate_proj,
+                                                                                         mlp.up_proj)))
+        return x, mlp(h, quantized=hq, fuse_quant=True)
 
 
 class LlamaForCausalLM(nn.Module):

@@ -81,7 +81,7 @@ def same_quantizer(a, b):
     if type(a) is not type(b):
         return False
     keys = ("ebit", "mbit", "sc_ebit", "sc_mbit", "block_size", "per_tensor_scale", "scale_allow_subnormal",
-            "use_round", "use_ceil", "l2_block_size", "l2_sc_bit", "l2_scheme")
+            "use_round", "use_ceil", "l2_block_size", "l2_sc_bit", "l2_scheme", "_fused")
     return all(getattr(a, k, None) == getattr(b, k, None) for k in keys)
 
 

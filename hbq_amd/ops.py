@@ -89,3 +89,16 @@ def stack_qkv_gemms(model):
             mod.stack_qkv = True
             n += 1
     return n
+
+
+def fuse_input_quantizers(model, on=True):
+    """Let every decoder layer of a model compute its linears' input quantizers inside the
+    passes that produce their inputs (RMSNorm -> q/k/v and gate/up, SiLU product -> down),
+    where those quantizers are HBQQuantizers that the fused kernels take; the outputs keep
+    their bits.  Returns the number of layers switched."""
+    n = 0
+    for mod in model.modules():
+        if hasattr(mod, "fuse_input_quant"):
+            mod.fuse_input_quant = bool(on)
+            n += 1
+    return n

@@ -386,10 +386,14 @@ class HBQQuantizer(MXFPQuantizer):
         if xc.numel():
             _lib.check(_lib.lib().hbq_hbq_qdq(
                 _lib.ptr(xc), _lib.ptr(y), _lib.ptr(l1), _lib.ptr(l2i), _lib.ptr(sch), _lib.ptr(codes), rows, cols,
-                _lib.DTYPE_CODE[x.dtype], B, self.ebit, self.mbit, self.sc_ebit, self.sc_mbit, self.l2_block_size,
-                self.l2_sc_bit, self.L2_SCHEME.index(self.l2_scheme), int(self.scale_allow_subnormal),
-                int(self.use_ceil), int(self._fused), _lib.stream_of(xc)), NotImplementedError)
+                _lib.DTYPE_CODE[x.dtype], *self.abi_args(), _lib.stream_of(xc)), NotImplementedError)
         return y.view(x.shape), codes, l1, l2i, sch
+
+    def abi_args(self):
+        """The quantizer's arguments of the C ABI, block_size .. compiled (include/hbq_amd.h)."""
+        return (self.block_size, self.ebit, self.mbit, self.sc_ebit, self.sc_mbit, self.l2_block_size,
+                self.l2_sc_bit, self.L2_SCHEME.index(self.l2_scheme), int(self.scale_allow_subnormal),
+                int(self.use_ceil), int(self._fused))
 
     def q(self, x: torch.Tensor):
         y, _, l1, l2i, sch = self._run_hbq(x, want_codes=False, want_stats=self.keep_l2_scale)

@@ -307,6 +307,24 @@ int hbq_rms_apply(const void *x, const float *rs, const void *w, void *y, int64_
  * a quantizer after the activation). */
 int hbq_silu_mul(const void *g, const void *u, void *y, int64_t n, int dtype, void *stream);
 
+/* No reference counterpart as kernels: the linears' input quantizer applied to the
+ * output of the pass that produces it (src/module.py:45-50, self.aq(x) of
+ * _QBaseLinear.forward, on the RMSNorm output that feeds q/k/v and gate/up and on the
+ * SiLU product that feeds down, src/module.py:547-569), in one pass whose producer
+ * output is never written.  y is bit for bit hbq_hbq_qdq(x = hbq_rms_apply(x, rs, w))
+ * and hbq_hbq_qdq(x = hbq_silu_mul(g, u)) with the same quantizer arguments; [rows,
+ * cols] row-major, fp16 / bf16.  Returns HBQ_ERR_UNSUPPORTED outside the fused kernels:
+ * E2M2 elements (mbit 2), one L2 scheme (not Mix), block_size 128, an E5M3 L1 scale
+ * without subnormals, cols % 128 == 0 and 16-byte aligned tensors. */
+int hbq_rms_apply_hbq_qdq(const void *x, const float *rs, const void *w, void *y, int64_t rows, int64_t cols,
+                          int dtype, int block_size, int ebit, int mbit, int sc_ebit, int sc_mbit, int l2_block_size,
+                          int l2_sc_bit, int l2_scheme, int scale_allow_subnormal, int use_ceil, int compiled,
+                          void *stream);
+int hbq_silu_mul_hbq_qdq(const void *g, const void *u, void *y, int64_t rows, int64_t cols, int dtype,
+                         int block_size, int ebit, int mbit, int sc_ebit, int sc_mbit, int l2_block_size,
+                         int l2_sc_bit, int l2_scheme, int scale_allow_subnormal, int use_ceil, int compiled,
+                         void *stream);
+
 /* No reference counterpart: dst[cols, rows] = src[rows, cols]^T for 16-bit
  * elements.  The blockquant_ext front end uses it to hand a B[K,N] operand to
  * the W[N,K] kernels. */

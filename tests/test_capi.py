@@ -118,3 +118,18 @@ def test_decoder_kernel_argument_errors_without_gpu(lib):
     assert L.hbq_silu_mul(fake, fake, fake, 16, 2, None) == 2
     assert L.hbq_silu_mul(fake, fake, fake, 20, 0, None) == 2
     assert L.hbq_silu_mul(None, None, None, 0, 1, None) == 0
+    # quantizer fused into the RMSNorm apply / SiLU product: only E2M2, one scheme, block 128
+    q = [128, 2, 2, 5, 3, 32, 2, 2, 0, 0, 1]                  # HBQ-E act (SIG-1), compiled rule
+
+    def with_(**kw):
+        names = ["block", "ebit", "mbit", "sc_ebit", "sc_mbit", "l2b", "l2bit", "scheme", "sub", "ceil", "comp"]
+        return [kw.get(n, v) for n, v in zip(names, q)]
+    for fn, lead in ((L.hbq_rms_apply_hbq_qdq, (fake, fake, fake, fake)), (L.hbq_silu_mul_hbq_qdq, (fake, fake, fake))):
+        assert fn(*lead, 4, 256, 2, *q, None) == 2                       # fp32
+        assert fn(*lead, 4, 256, 0, *with_(mbit=1), None) == 2
+        assert fn(*lead, 4, 256, 0, *with_(scheme=7), None) == 2        # Mix
+        assert fn(*lead, 4, 256, 0, *with_(block=64), None) == 2
+        assert fn(*lead, 4, 256, 0, *with_(ebit=3), None) == 2
+        assert fn(*lead, 4, 200, 0, *q, None) != 0                       # cols % 128
+        assert fn(*((None,) * len(lead)), 0, 256, 0, *q, None) == 0      # empty: no-op
+        assert fn(*((None,) * len(lead)), 4, 256, 0, *q, None) == 1

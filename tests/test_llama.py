@@ -364,3 +364,105 @@ def test_causal_quantizer_equals_full(gpu, dt):
             assert got is pin                   # the in-place kernel ran
             same = got.view(torch.int16) == ref.view(torch.int16)
             assert bool(same.all()), (T, qz.l2_scheme, qz.l2_block_size, int((~same).sum()))
+
+
+# activation quantizers that the fused producer passes take (E2M2, one L2 scheme, block 128)
+FUSED_QZ = [dict(l2_block_size=8, l2_sc_bit=2, l2_scheme="SIG-1"),                        # HBQ-A act
+            dict(l2_block_size=32, l2_sc_bit=2, l2_scheme="SIG-1"),                       # HBQ-E act
+            dict(l2_block_size=16, l2_sc_bit=1, l2_scheme="FP-1", use_quant_kernel=False),
+            dict(l2_block_size=8, l2_sc_bit=2, l2_scheme="PoT", use_ceil=True)]
+
+
+def _fused_qz(kw):
+    return Q.HBQQuantizer(block_size=128, ebit=2, mbit=2, sc_ebit=5, sc_mbit=3, **kw)
+
+
+def _same16(got, ref, what):
+    same = got.view(torch.int16) == ref.view(torch.int16)
+    assert bool(same.all()), (what, int((~same).sum()), (~same).nonzero()[:4].tolist())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_rms_apply_quant_equals_two_passes(gpu, dt):
+    """The RMSNorm apply step with the input quantizer in the same pass gives aq.q(norm(x +
+    res)) bit for bit, the sum too; rows of tiny, huge, infinite and NaN values included."""
+    from hbq_amd.llama import RMSNorm
+    g = torch.Generator(device=gpu).manual_seed(31)
+    for cols in (1024, 4096):
+        norm = RMSNorm(cols, 1e-5).to(gpu).to(dt)
+        with torch.no_grad():
+            norm.weight.copy_(torch.randn(cols, device=gpu, generator=g) * 0.5 + 1)
+        x = (torch.randn(37, cols, device=gpu, generator=g) * 3).to(dt)
+        res = (torch.randn(37, cols, device=gpu, generator=g) * 2).to(dt)
+        x[0, :] = x[0, :] * 1e-3
+        x[1, :] = 60000.0 if dt == torch.float16 else 1e30
+        x[4, ::7] *= 80.0                                   # outlier channels
+        res[2, 5] = float("inf")
+        res[3, 7] = float("nan")
+        for kw in FUSED_QZ:
+            qz = _fused_qz(kw)
+            with torch.no_grad():
+                s, yq, done = norm.add_norm_quant(x, res, qz)
+                s_ref, y_ref = norm.add_norm(x, res)
+                ref = qz.q(y_ref)
+                y0, done0 = norm.add_norm_quant(x, None, qz)[1:]
+                ref0 = qz.q(norm.add_norm(x)[1])
+            assert done and done0, kw
+            _same16(s, s_ref, ("sum", cols, kw))
+            _same16(yq, ref, ("norm + quantizer", cols, kw))
+            _same16(y0, ref0, ("norm alone + quantizer", cols, kw))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_silu_mul_quant_equals_two_passes(gpu, dt):
+    """silu(gate) * up with the input quantizer in the same pass gives aq.q(silu_mul(gate,
+    up)) bit for bit: every 16-bit pattern of the gate, and a [37, 14336] MLP-shaped input."""
+    from hbq_amd.llama import silu_mul, silu_mul_quant
+    g = torch.Generator(device=gpu).manual_seed(32)
+    gate_all = torch.arange(-32768, 32768, dtype=torch.int32, device=gpu).to(torch.int16).view(dt).view(512, 128)
+    cases = [(gate_all, (torch.randn(512, 128, device=gpu, generator=g) * 4).to(dt)),
+             ((torch.randn(37, 14336, device=gpu, generator=g) * 2).to(dt),
+              (torch.randn(37, 14336, device=gpu, generator=g)).to(dt))]
+    for gate, up in cases:
+        for kw in FUSED_QZ:
+            qz = _fused_qz(kw)
+            got = silu_mul_quant(gate, up, qz)
+            assert got is not None, kw
+            _same16(got, qz.q(silu_mul(gate, up)), (tuple(gate.shape), kw))
+
+
+@pytest.mark.gpu
+def test_fused_input_quantizers_same_logits(gpu):
+    """A prefill with the linears' input quantizers computed inside the norms and the SiLU
+    product gives the logits of the separate passes bit for bit, with three fewer quantizer
+    passes per layer (q/k/v, gate/up and down inputs)."""
+    from hbq_amd.ops import fuse_input_quantizers, stack_qkv_gemms, use_hip_fp32_gemm
+    m = LlamaForCausalLM(TINY).random_init_(seed=6).half().to(gpu)
+    p = PTQ(hbq_cfg(kv=True), m)
+    p.inject_quantizers()
+    p.static_quant_wgt()
+    use_hip_fp32_gemm(m)
+    stack_qkv_gemms(m)
+    ids = torch.randint(0, TINY.vocab_size, (1, 256), device=gpu, generator=torch.Generator(device=gpu).manual_seed(6))
+    calls = []
+    orig = Q.HBQQuantizer.q
+
+    def counting(self, x):
+        calls.append(1)
+        return orig(self, x)
+    Q.HBQQuantizer.q = counting
+    try:
+        with torch.no_grad():
+            ref = m(ids)
+            n_sep = len(calls)
+            assert fuse_input_quantizers(m) == TINY.num_hidden_layers
+            calls.clear()
+            out = m(ids)
+            n_fused = len(calls)
+    finally:
+        Q.HBQQuantizer.q = orig
+        fuse_input_quantizers(m, on=False)
+    assert n_sep - n_fused == 3 * TINY.num_hidden_layers, (n_sep, n_fused)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
