@@ -150,6 +150,10 @@ __global__ void build_lut_kernel(int slot, FastParams p) {
 template <class T>
 constexpr int fast_threads() { return T::dt == kF16 ? 512 : 256; }
 
+// The in-place quantizer of causal attention weights (memory input, causal_t > 0) is
+// its own instantiation, so that the plain memory-input kernel can prefetch.
+constexpr int kSrcXCausal = 3;
+
 // Block 128 (8 lanes x 16 elements).  Per-wave magnitude tables, laid out
 // [scheme][candidate][block-in-wave][level] with rows padded by one entry so
 // that the eight blocks of a wave fall on different LDS banks.
@@ -202,16 +206,34 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
     const int64_t ntiles = (nb + blocks_per_wg - 1) / blocks_per_wg;
     const float tiny = T::dt == kF16 ? 6.103515625e-05f : 1.17549435e-38f;
 
-    // causal_t > 0: nb blocks of [mats, t, t] attention weights whose blocks above the
-    // diagonal are zero and stay as they are (y == x): each wave takes one column block of
-    // 8 consecutive rows among the blocks on or below the diagonal.  Rows 128k .. 128k+127
-    // of a matrix (band k, 16 groups of 8 rows) hold k + 1 such blocks.
+    // causal_t > 0 (kSrcXCausal only): nb blocks of [mats, t, t] attention weights whose
+    // blocks above the diagonal are zero and stay as they are (y == x): each wave takes one
+    // column block of 8 consecutive rows among the blocks on or below the diagonal.  Rows
+    // 128k .. 128k+127 of a matrix (band k, 16 groups of 8 rows) hold k + 1 such blocks.
+    if constexpr (SRC != kSrcXCausal) causal_t = 0;
+    constexpr bool kMem = SRC == kSrcX || SRC == kSrcXCausal;
     const int64_t nbt = causal_t / block;
     const int64_t per_mat = 8 * nbt * (nbt + 1);
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int64_t nwork = causal_t ? nb / (causal_t * nbt) * per_mat : ntiles;
     const int64_t first = causal_t ? (int64_t)blockIdx.x * (NTH / 64) + wave : (int64_t)blockIdx.x;
     const int64_t stride = causal_t ? (int64_t)gridDim.x * (NTH / 64) : (int64_t)gridDim.x;
+
+    // memory input in row order: the next tile's 16 elements per lane are loaded while this
+    // tile is worked on.  The loads are unconditional (past the end a lane reads its current
+    // block again, or block 0, and the data is replaced by zeros), so that no branch around
+    // them makes the compiler wait for them before this tile's work.
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+    constexpr bool kPrefetch = SRC == kSrcX;
+    u32x4_t pf0 = {0u, 0u, 0u, 0u}, pf1 = {0u, 0u, 0u, 0u};
+    auto prefetch = [&](int64_t t, int64_t g_cur) __attribute__((always_inline)) {
+        const int64_t g = t * blocks_per_wg + (threadIdx.x / lpb);
+        const int64_t gc = (t < nwork && g < nb) ? g : g_cur;
+        const u32x4_t* q = reinterpret_cast<const u32x4_t*>(x + gc * (int64_t)block + (int64_t)li * kV);
+        pf0 = __builtin_nontemporal_load(q);
+        pf1 = __builtin_nontemporal_load(q + 1);
+    };
+    if constexpr (kPrefetch) prefetch(first, 0);
 
     for (int64_t tile = first; tile < nwork; tile += stride) {
         int64_t gb;
@@ -231,9 +253,12 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
 
         // load 16 elements; the block max of |x| over the raw 16-bit patterns
         uint32_t w[8];
-        if (valid) {
-            typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-            if constexpr (SRC == kSrcX) {
+        if constexpr (kPrefetch) {
+            w[0] = valid ? pf0.x : 0u; w[1] = valid ? pf0.y : 0u; w[2] = valid ? pf0.z : 0u; w[3] = valid ? pf0.w : 0u;
+            w[4] = valid ? pf1.x : 0u; w[5] = valid ? pf1.y : 0u; w[6] = valid ? pf1.z : 0u; w[7] = valid ? pf1.w : 0u;
+            prefetch(tile + stride, valid ? gb : 0);
+        } else if (valid) {
+            if constexpr (kMem) {
                 const u32x4_t* q = reinterpret_cast<const u32x4_t*>(x + off);
                 const u32x4_t a = __builtin_nontemporal_load(q), b = __builtin_nontemporal_load(q + 1);
                 w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
@@ -547,6 +572,9 @@ int launch_fast(const void* x, void* y, void* l1, void* l2i, void* sch, void* co
     const size_t lds = (size_t)S * (p.n + 2) * 4 +
                        (size_t)(NTH >> lpb_log2) * S * kFastJ * ((1 << (M + 2)) + 1) * sizeof(DTabT<T>);
     if (lds > 160 * 1024) return 0;
+    if constexpr (SRC == kSrcX) {
+        if (causal_t) return launch_fast<T, M, L2B, S, kSrcXCausal>(x, y, l1, l2i, sch, codes, nb, causal_t, slot, p, dev, st);
+    }
     auto kern = hbq_fast_kernel<T, M, L2B, S, SRC>;
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, NTH, lds) != hipSuccess || per_cu <= 0)
