@@ -483,7 +483,7 @@ int hbq_gemm_fp32_accum_batched(const void* A, const void* W, void* C, int64_t b
     hbq_clear_error();
     if (batches < 0) return hbq_fail(HBQ_ERR_INVALID, "negative batch count");
     if (int rc = check_shapes(A, W, C, M, N, K)) return rc;
-    if (batches > 65535) return hbq_fail(HBQ_ERR_INVALID, "too many batches");
+    if (batches > 0x7fffffff) return hbq_fail(HBQ_ERR_INVALID, "too many batches");
     if (stride_a < M * K || stride_w < N * K || stride_c < M * N)
         return hbq_fail(HBQ_ERR_INVALID, "batch strides smaller than one problem");
     hipStream_t st = (hipStream_t)stream;

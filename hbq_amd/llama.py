@@ -304,6 +304,8 @@ class QLlamaAttention(nn.Module):
         if self.quant_attn_wgt:
             p = quantize_causal_(self.attn_wgt_quantizer, p)
         pg = p.view(b, kvh, (H // kvh) * T, T)
+        if vT is not None and not (pg.dtype == torch.float16 and pg.is_contiguous() and pg.data_ptr() % 16 == 0):
+            v, vT = vT.transpose(-1, -2).contiguous(), None   # the quantizer returned another layout
         out = _batched_gemm(pg, vT) if vT is not None else torch.matmul(pg, v)
         return out.view(b, H, T, d), p
 

@@ -182,14 +182,16 @@ class _QBaseLinear(nn.Linear):
         # the weight was quantized in place before inference (src/ptq.py:338-358)
         return self.forward_quantized(self.aq(x))
 
-    def gemm_weight(self) -> torch.Tensor:
+    def gemm_weight(self, copy: bool = False) -> torch.Tensor:
         """The weight the GEMM reads: the parameter, or for a packed weight
-        (hbq_amd.packed.pack_linear_weights) its decoded fake-quantized values."""
+        (hbq_amd.packed.pack_linear_weights) its decoded fake-quantized values, which live
+        in a scratch buffer that the next decode of that shape on the stream overwrites
+        (copy=True: a tensor of its own, for use outside the forward)."""
         p = self.__dict__.get("packed_weight")
         if p is None:
             return self.weight
         from .packed import decoded_weight
-        return decoded_weight(p)
+        return decoded_weight(p, copy=copy)
 
     def forward_quantized(self, xq: torch.Tensor) -> torch.Tensor:
         """forward() on an input already quantized by a quantizer equal to self.aq."""

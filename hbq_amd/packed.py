@@ -161,20 +161,22 @@ _SCRATCH = {}
 
 
 def _scratch(shape, dtype, device):
-    """One decode buffer per (shape, dtype, device), reused by every layer of that shape:
-    layers run one after another on one stream, so a buffer is free again once the GEMM
-    that read it has been issued after it."""
-    key = (tuple(shape), dtype, device)
+    """One decode buffer per (shape, dtype, device, stream), reused by every layer of that
+    shape: calls on one stream run in order, so a buffer is free again once the GEMM that
+    read it has been issued after it; another stream gets its own buffer."""
+    key = (tuple(shape), dtype, device, torch.cuda.current_stream(device).cuda_stream)
     buf = _SCRATCH.get(key)
     if buf is None:
         buf = _SCRATCH[key] = torch.empty(shape, dtype=dtype, device=device)
     return buf
 
 
-def decoded_weight(p: PackedHBQ) -> torch.Tensor:
+def decoded_weight(p: PackedHBQ, copy: bool = False) -> torch.Tensor:
     """The fake-quantized weight of a packed linear, decoded into the shared scratch buffer
-    of its shape (valid until the next decode of that shape on the stream)."""
-    return unpack(p, _scratch(p.shape, p.dtype, p.codes.device))
+    of its shape and stream: valid until the next decode of that shape on that stream
+    (copy=True returns a tensor of its own)."""
+    w = unpack(p, _scratch(p.shape, p.dtype, p.codes.device))
+    return w.clone() if copy else w
 
 
 def decoded_stack(ps) -> torch.Tensor:

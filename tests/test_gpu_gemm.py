@@ -331,3 +331,25 @@ def test_fp32_batched_equals_per_problem(gpu, Z, M, N, K):
     for z in range(Z):
         ref = ext.gemm_fp32_accum_nk(A[z], W[z])
         assert torch.equal(C[z].view(torch.int16), ref.view(torch.int16)), z
+
+
+def test_fp32_batched_strides_beyond_one_problem(gpu):
+    """Batch strides larger than one problem (problems inside wider buffers, as the ABI
+    allows): each problem gets the bits of the single GEMM, and the gaps of C stay as
+    they were."""
+    from hbq_amd import _lib, blockquant_ext as ext
+    Z, M, N, K = 4, 320, 256, 192
+    sA, sW, sC = M * K + 136, N * K + 64, M * N + 8
+    g = torch.Generator(device=gpu).manual_seed(77)
+    A = torch.randn(Z * sA, device=gpu, generator=g).half()
+    W = (torch.randn(Z * sW, device=gpu, generator=g) * 0.1).half()
+    C = torch.full((Z * sC,), 7.0, device=gpu, dtype=torch.float16)
+    _lib.check(_lib.lib().hbq_gemm_fp32_accum_batched(_lib.ptr(A), _lib.ptr(W), _lib.ptr(C), Z, M, N, K, sA, sW,
+                                                      sC, _lib.stream_of(A)))
+    for z in range(Z):
+        a = A[z * sA: z * sA + M * K].view(M, K)
+        w = W[z * sW: z * sW + N * K].view(N, K)
+        ref = ext.gemm_fp32_accum_nk(a, w)
+        got = C[z * sC: z * sC + M * N].view(M, N)
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), z
+        assert bool((C[z * sC + M * N: (z + 1) * sC] == 7.0).all()), z
