@@ -335,8 +335,11 @@ int launch_mx_fast(const void* x, void* y, void* scales, void* codes, int64_t n_
         return 0;
     const int64_t ntiles = (n_elems + 1023) / 1024;
     const int64_t waves_needed = ntiles;
-    const int64_t resident = (int64_t)g_mx_cus[dev] * per_cu * (kMxThreads / 64);
-    // as many rounds as the resident waves need, with the tiles spread evenly over them
+    // twice the waves that fit at once: the workgroups beyond them start as the first ones
+    // finish, which staggers the waves' load / compute phases (configs[1]: 2 tiles a wave
+    // instead of 3; MXFP4 17.7 -> 16.9 us, NVFP4 18.6 -> 17.4 us, MXFP8 within 1%)
+    const int64_t resident = 2 * (int64_t)g_mx_cus[dev] * per_cu * (kMxThreads / 64);
+    // as many rounds as those waves need, with the tiles spread evenly over them
     const int64_t rounds = (waves_needed + resident - 1) / resident;
     const int64_t waves = (waves_needed + rounds - 1) / rounds;
     const int64_t grid = (waves + kMxThreads / 64 - 1) / (kMxThreads / 64);
