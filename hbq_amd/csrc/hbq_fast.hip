@@ -220,16 +220,17 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
     const int64_t stride = causal_t ? (int64_t)gridDim.x * (NTH / 64) : (int64_t)gridDim.x;
 
     // memory input in row order: the next tile's 16 elements per lane are loaded while this
-    // tile is worked on.  The loads are unconditional (past the end a lane reads its current
-    // block again, or block 0, and the data is replaced by zeros), so that no branch around
-    // them makes the compiler wait for them before this tile's work.
+    // tile is worked on.  No lane branches around the loads (a lane past the end of the
+    // last tile reads its current block again and the data is replaced by zeros), and no
+    // other path writes their registers, so the compiler waits for them only where the next
+    // tile reads them; after the wave's last tile none are issued (a wave-uniform branch).
     typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
     constexpr bool kPrefetch = SRC == kSrcX;
     u32x4_t pf0 = {0u, 0u, 0u, 0u}, pf1 = {0u, 0u, 0u, 0u};
     auto prefetch = [&](int64_t t, int64_t g_cur) __attribute__((always_inline)) {
+        if (t >= nwork) return;
         const int64_t g = t * blocks_per_wg + (threadIdx.x / lpb);
-        const int64_t gc = (t < nwork && g < nb) ? g : g_cur;
-        const u32x4_t* q = reinterpret_cast<const u32x4_t*>(x + gc * (int64_t)block + (int64_t)li * kV);
+        const u32x4_t* q = reinterpret_cast<const u32x4_t*>(x + (g < nb ? g : g_cur) * (int64_t)block + (int64_t)li * kV);
         pf0 = __builtin_nontemporal_load(q);
         pf1 = __builtin_nontemporal_load(q + 1);
     };
