@@ -28,6 +28,7 @@ SIGNATURES = {
     "hbq_gemm_fp32_accum_ws": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P], _I),
     "hbq_gemm_fp32_accum_noalloc": ([_P, _P, _P, _I64, _I64, _I64, _I, _P], _I),
     "hbq_gemm_fp32_accum_batched": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P], _I),
+    "hbq_gemm_fp32_accum_batched_ex": ([_P, _P, _P] + [_I64] * 9 + [_P], _I),
     "hbq_gemm_fp32_accum": ([_P, _P, _P, _I64, _I64, _I64, _I, _P], _I),
     "hbq_gemm_fp16_accum": ([_P, _P, _P, _I64, _I64, _I64, _I, _P], _I),
     "hbq_gemm_fp16_grouped_accum": ([_P, _P, _P, _I64, _I64, _I64, _I, _I, _P], _I),

@@ -478,25 +478,45 @@ int hbq_gemm_fp32_accum_ws(const void* A, const void* B, void* C, void* ws, int6
     return hbq_check_launch("gemm_fp32_accum");
 }
 
-int hbq_gemm_fp32_accum_batched(const void* A, const void* W, void* C, int64_t batches, int64_t M, int64_t N,
-                                int64_t K, int64_t stride_a, int64_t stride_w, int64_t stride_c, void* stream) {
+int hbq_gemm_fp32_accum_batched_ex(const void* A, const void* W, void* C, int64_t batches, int64_t M, int64_t N,
+                                   int64_t K, int64_t stride_a, int64_t stride_w, int64_t w_group, int64_t stride_c,
+                                   int64_t ldc, void* stream) {
     hbq_clear_error();
     if (batches < 0) return hbq_fail(HBQ_ERR_INVALID, "negative batch count");
     if (int rc = check_shapes(A, W, C, M, N, K)) return rc;
     if (batches > 0x7fffffff) return hbq_fail(HBQ_ERR_INVALID, "too many batches");
-    if (stride_a < M * K || stride_w < N * K || stride_c < M * N)
-        return hbq_fail(HBQ_ERR_INVALID, "batch strides smaller than one problem");
+    if (w_group < 1 || w_group > 0x7fffffff) return hbq_fail(HBQ_ERR_INVALID, "w_group must be at least 1");
+    if (ldc < N) return hbq_fail(HBQ_ERR_INVALID, "ldc smaller than N");
+    if (stride_a < M * K || stride_w < N * K) return hbq_fail(HBQ_ERR_INVALID, "batch strides smaller than one problem");
+    // the problems' outputs must not overlap: one after another, or interleaved within the rows
+    const bool apart = M == 0 || stride_c >= (M - 1) * ldc + N;
+    const bool interleaved = stride_c >= N && (batches - 1) * stride_c + N <= ldc;
+    if (batches > 1 && !apart && !interleaved) return hbq_fail(HBQ_ERR_INVALID, "the problems' outputs overlap");
     hipStream_t st = (hipStream_t)stream;
     if (batches == 0 || M == 0 || N == 0) return 0;
     if (K == 0) {
+        if (ldc != N) return hbq_fail(HBQ_ERR_UNSUPPORTED, "K == 0 with ldc != N");
         for (int64_t z = 0; z < batches; ++z) zero_output((uint16_t*)C + z * stride_c, M, N, st);
         return hbq_check_launch("gemm_fp32_accum_batched");
     }
-    if (!launch_batched_fp32(A, W, C, (int)batches, (int)M, (int)N, (int)K, stride_a, stride_w, stride_c, st))
+    if (!launch_batched_fp32(A, W, C, (int)batches, (int)M, (int)N, (int)K, stride_a, stride_w, stride_c, (int)w_group,
+                             ldc, st)) {
+        if (ldc != N)
+            return hbq_fail(HBQ_ERR_UNSUPPORTED, "ldc != N needs K %% 64 == 0, N %% 8 == 0 and 16-byte aligned rows");
         for (int64_t z = 0; z < batches; ++z)
-            launch_any<kFp32, 4>((const uint16_t*)A + z * stride_a, (const uint16_t*)W + z * stride_w,
+            launch_any<kFp32, 4>((const uint16_t*)A + z * stride_a, (const uint16_t*)W + (z / w_group) * stride_w,
                                  (uint16_t*)C + z * stride_c, nullptr, (int)M, (int)N, (int)K, (int)K, 1, st);
+    }
     return hbq_check_launch("gemm_fp32_accum_batched");
+}
+
+int hbq_gemm_fp32_accum_batched(const void* A, const void* W, void* C, int64_t batches, int64_t M, int64_t N,
+                                int64_t K, int64_t stride_a, int64_t stride_w, int64_t stride_c, void* stream) {
+    if (stride_c < M * N) {
+        hbq_clear_error();
+        return hbq_fail(HBQ_ERR_INVALID, "batch strides smaller than one problem");
+    }
+    return hbq_gemm_fp32_accum_batched_ex(A, W, C, batches, M, N, K, stride_a, stride_w, 1, stride_c, N, stream);
 }
 
 int hbq_gemm_fp16_accum(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int b_is_nk,

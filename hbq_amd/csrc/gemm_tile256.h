@@ -17,9 +17,10 @@ int splitk_fp32_splits(int M, int N, int K);
 int launch_splitk_fp32(const void* A, const void* W, void* C, float* ws, int M, int N, int K, int splits,
                        hipStream_t st);
 
-// fp32 accumulation over `batches` independent problems C_z = A_z W_z^T (element
-// strides sA, sW, sC between them) in one launch; 0 when the layout does not allow it.
+// fp32 accumulation over `batches` independent problems C_z = A_z W_{z / wgroup}^T
+// (element strides sA, sW, sC between them; row stride ldc of C) in one launch; 0 when
+// the layout does not allow it.
 int launch_batched_fp32(const void* A, const void* W, void* C, int batches, int M, int N, int K, int64_t sA,
-                        int64_t sW, int64_t sC, hipStream_t st);
+                        int64_t sW, int64_t sC, int wgroup, int64_t ldc, hipStream_t st);
 
 }  // namespace hbq_gemm

@@ -49,7 +49,7 @@ template <int MODE, int GN, bool SMALLG, int GS, int SPG, int TN>
 __global__ __launch_bounds__(NT, 1) void kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ W,
                                                 uint16_t* __restrict__ C, float* __restrict__ P, int M, int N, int K,
                                                 int gk, int tiles_m, int tiles_n, int splits, int batches,
-                                                int64_t sA, int64_t sW, int64_t sC) {
+                                                int64_t sA, int64_t sW, int64_t sC, int wgroup, int64_t ldc) {
     constexpr int WSL = TN * TK;          // halfs of one W slice
     constexpr int NWN = TN / 64;          // waves across the tile's columns
     constexpr int WROWS = TM * NWN / 8;   // rows of one wave (128 or 64)
@@ -79,7 +79,7 @@ __global__ __launch_bounds__(NT, 1) void kernel(const uint16_t* __restrict__ A, 
         const int z = u / T;
         u -= z * T;
         A += z * sA;
-        W += z * sW;
+        W += (z / wgroup) * sW;   // problems z of one W group share W (grouped-query attention)
         C += z * sC;
     }
     if ((T & 7) == 0) u = (u & 7) * (T >> 3) + (u >> 3);
@@ -278,18 +278,21 @@ __global__ __launch_bounds__(NT, 1) void kernel(const uint16_t* __restrict__ A, 
         const int row = id >> 3, ch = id & 7;
         const u32x4 v = *reinterpret_cast<const u32x4*>(st + swz(row, ch));
         const int m = m0 + wm + row, n = n0 + wn + 8 * ch;
-        if (m < M && n < N) *reinterpret_cast<u32x4*>(C + (int64_t)m * N + n) = v;
+        if (m < M && n < N) *reinterpret_cast<u32x4*>(C + (int64_t)m * ldc + n) = v;
     }
 }
 
 template <int MODE, int GN, int TN>
 void launch(const void* A, const void* W, void* C, float* P, int M, int N, int K, int gk, hipStream_t st,
-            int splits = 1, int batches = 1, int64_t sA = 0, int64_t sW = 0, int64_t sC = 0) {
+            int splits = 1, int batches = 1, int64_t sA = 0, int64_t sW = 0, int64_t sC = 0, int wgroup = 1,
+            int64_t ldc = 0) {
     const int tm = (M + TM - 1) / TM, tn = (N + TN - 1) / TN;
+    if (ldc == 0) ldc = N;
     const dim3 grid(tm * tn * (splits > batches ? splits : batches)), block(NT);
 #define T256_LAUNCH(SM, GS_, SPG_)                                                                              \
     hipLaunchKernelGGL((kernel<MODE, GN, SM, GS_, SPG_, TN>), grid, block, 0, st, (const uint16_t*)A,          \
-                       (const uint16_t*)W, (uint16_t*)C, P, M, N, K, gk, tm, tn, splits, batches, sA, sW, sC)
+                       (const uint16_t*)W, (uint16_t*)C, P, M, N, K, gk, tm, tn, splits, batches, sA, sW, sC, wgroup,  \
+                       ldc)
     if constexpr (MODE == kFp32) {
         T256_LAUNCH(false, 4, 1);
     } else {
@@ -394,16 +397,16 @@ int launch_splitk_fp32(const void* A, const void* W, void* C, float* ws, int M, 
 }
 
 int launch_batched_fp32(const void* A, const void* W, void* C, int batches, int M, int N, int K, int64_t sA,
-                        int64_t sW, int64_t sC, hipStream_t st) {
+                        int64_t sW, int64_t sC, int wgroup, int64_t ldc, hipStream_t st) {
     using namespace t256;
-    if (batches < 1 || M < 1 || N < 1 || K % TK != 0 || N % 8 != 0) return 0;
-    if (((uintptr_t)A | (uintptr_t)W | (uintptr_t)C) % 16 != 0 || (sA | sW | sC) % 8 != 0) return 0;
+    if (batches < 1 || M < 1 || N < 1 || K % TK != 0 || N % 8 != 0 || wgroup < 1 || ldc < N) return 0;
+    if (((uintptr_t)A | (uintptr_t)W | (uintptr_t)C) % 16 != 0 || (sA | sW | sC | ldc) % 8 != 0) return 0;
     if ((int64_t)M * K >= (1ll << 31) || (int64_t)N * K >= (1ll << 31)) return 0;
-    if (sA < (int64_t)M * K || sW < (int64_t)N * K || sC < (int64_t)M * N) return 0;
+    if (sA < (int64_t)M * K || sW < (int64_t)N * K) return 0;
     const int64_t tiles = (int64_t)batches * ((M + TM - 1) / TM) * ((N + 255) / 256);
     if (tiles * 2 > 0x7fffffffll) return 0;
-    if (N <= 128) launch<kFp32, 4, 128>(A, W, C, nullptr, M, N, K, K, st, 1, batches, sA, sW, sC);
-    else launch<kFp32, 4, 256>(A, W, C, nullptr, M, N, K, K, st, 1, batches, sA, sW, sC);
+    if (N <= 128) launch<kFp32, 4, 128>(A, W, C, nullptr, M, N, K, K, st, 1, batches, sA, sW, sC, wgroup, ldc);
+    else launch<kFp32, 4, 256>(A, W, C, nullptr, M, N, K, K, st, 1, batches, sA, sW, sC, wgroup, ldc);
     return 1;
 }
 

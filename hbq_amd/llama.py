@@ -223,6 +223,28 @@ def _batched_gemm(a, w):
     return c
 
 
+def _pv_into_bthd(p, vT):
+    """out [b, T, H, d] (contiguous) = P V for the attention weights p [b, H, T, T] and the
+    quantized V^T [b, KVH, d, T]: one hbq_gemm_fp32_accum_batched_ex launch per batch entry
+    over the H query heads, each writing its [T, d] output at column h * d of the rows of
+    the o projection's input (the bits of _batched_gemm; no transpose copy).  None when
+    the operands do not fit."""
+    b, H, T, _ = p.shape
+    kvh, d = vT.shape[1], vT.shape[2]
+    if not (p.dtype == torch.float16 and vT.dtype == torch.float16 and p.is_contiguous() and vT.is_contiguous()
+            and p.data_ptr() % 16 == 0 and vT.data_ptr() % 16 == 0 and T % 64 == 0 and d % 8 == 0 and H % kvh == 0):
+        return None
+    out = torch.empty((b, T, H, d), dtype=torch.float16, device=p.device)
+    st = _lib.stream_of(p)
+    for i in range(b):
+        rc = _lib.lib().hbq_gemm_fp32_accum_batched_ex(_lib.ptr(p[i]), _lib.ptr(vT[i]), _lib.ptr(out[i]), H, T, d, T,
+                                                        T * T, d * T, H // kvh, d, H * d, st)
+        if rc == _lib.ERR_UNSUPPORTED:
+            return None
+        _lib.check(rc)
+    return out
+
+
 def _rope_ok(x):
     return (x.is_cuda and x.dtype in (torch.float16, torch.bfloat16) and x.shape[-1] % 16 == 0
             and x.stride(-1) == 1 and all(st % 8 == 0 for st in x.stride()[:-1]) and x.data_ptr() % 16 == 0)
@@ -272,14 +294,16 @@ class QLlamaAttention(nn.Module):
         # one GEMM over the stacked q/k/v weights when their operators allow it (same bits)
         self.stack_qkv = False
 
-    def manual_sdpa(self, q, k, v, vT=None):
+    def manual_sdpa(self, q, k, v, vT=None, out_bthd=False):
         """Causal softmax(q k^T / sqrt(d)) v with the attention weights quantized after the
         softmax (src/module.py:93-117).  q [b, H, T, d]; k, v [b, KVH, T, d] with the query
         heads of one kv head consecutive (repeat_kv's order): each kv head's rep = H / KVH
         query heads multiply it as one [rep * T, d] operand, which reads the same scores and
         outputs as the repeated k and v without copying them.  With vT = v^T [b, KVH, d, T]
         contiguous (and v None) on the GPU, both products run on the HIP fp32-accumulation
-        GEMM, batched over the kv heads: k and vT are its W[N, K] operands as they lie."""
+        GEMM, batched over the kv heads: k and vT are its W[N, K] operands as they lie.
+        out_bthd: return the output as [b, T, H, d] (the o projection's input layout),
+        written there by the P V product where it can."""
         b, H, T, d = q.shape
         kvh = k.shape[1]
         scale = 1.0 / math.sqrt(d)
@@ -303,11 +327,16 @@ class QLlamaAttention(nn.Module):
             p = torch.softmax(s, dim=-1)
         if self.quant_attn_wgt:
             p = quantize_causal_(self.attn_wgt_quantizer, p)
+        if out_bthd and vT is not None:
+            out = _pv_into_bthd(p, vT)
+            if out is not None:
+                return out, p
         pg = p.view(b, kvh, (H // kvh) * T, T)
         if vT is not None and not (pg.dtype == torch.float16 and pg.is_contiguous() and pg.data_ptr() % 16 == 0):
             v, vT = vT.transpose(-1, -2).contiguous(), None   # the quantizer returned another layout
         out = _batched_gemm(pg, vT) if vT is not None else torch.matmul(pg, v)
-        return out.view(b, H, T, d), p
+        out = out.view(b, H, T, d)
+        return (out.transpose(1, 2).contiguous() if out_bthd else out), p
 
     def forward(self, x, cos, sin, quantized=False):
         """quantized: x is already q_proj.aq's output (the quantizer shared by q, k and v)."""
@@ -339,9 +368,8 @@ class QLlamaAttention(nn.Module):
         vT = v.transpose(-1, -2).contiguous()
         if self.quant_v_cache:
             vT = self.kv_quantizer.q(vT)
-        out, _ = self.manual_sdpa(q.contiguous(), k.contiguous(), None, vT=vT)
-        out = out.transpose(1, 2).contiguous().view(b, T, -1)
-        return self.o_proj(out)
+        out, _ = self.manual_sdpa(q.contiguous(), k.contiguous(), None, vT=vT, out_bthd=True)
+        return self.o_proj(out.view(b, T, -1))
 
 
 class QLlamaMLP(nn.Module):

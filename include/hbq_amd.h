@@ -224,6 +224,18 @@ int hbq_gemm_fp32_accum_noalloc(const void *A, const void *B, void *C, int64_t M
 int hbq_gemm_fp32_accum_batched(const void *A, const void *W, void *C, int64_t batches, int64_t M, int64_t N,
                                 int64_t K, int64_t stride_a, int64_t stride_w, int64_t stride_c, void *stream);
 
+/* No reference counterpart: hbq_gemm_fp32_accum_batched with problems z of one group of
+ * w_group sharing W (W_z at (z / w_group) * stride_w: grouped-query attention, the
+ * query heads of one kv head) and C rows ldc elements apart, so that P.V writes the
+ * attention output straight into the [tokens, heads, head_dim] layout the o projection
+ * reads (C_h at h * head_dim, ldc = heads * head_dim).  The outputs must not overlap:
+ * stride_c >= (M - 1) ldc + N, or stride_c >= N with (batches - 1) stride_c + N <= ldc.
+ * ldc != N needs K % 64 == 0, N % 8 == 0 and 16-byte aligned rows (else
+ * HBQ_ERR_UNSUPPORTED). */
+int hbq_gemm_fp32_accum_batched_ex(const void *A, const void *W, void *C, int64_t batches, int64_t M, int64_t N,
+                                   int64_t K, int64_t stride_a, int64_t stride_w, int64_t w_group, int64_t stride_c,
+                                   int64_t ldc, void *stream);
+
 /* Replaces gemm_fp16_accum -> gemm_fp16_accum_cuda (blockquant_ext.cpp:31-39, gemm.cu:568-591):
  * one fused fp16 multiply-add per k in ascending order (bit-exact for any input). */
 int hbq_gemm_fp16_accum(const void *A, const void *B, void *C, int64_t M, int64_t N, int64_t K, int b_is_nk,

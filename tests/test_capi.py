@@ -118,6 +118,14 @@ def test_decoder_kernel_argument_errors_without_gpu(lib):
     assert L.hbq_silu_mul(fake, fake, fake, 16, 2, None) == 2
     assert L.hbq_silu_mul(fake, fake, fake, 20, 0, None) == 2
     assert L.hbq_silu_mul(None, None, None, 0, 1, None) == 0
+    # batched GEMM with shared W groups and a C row stride: argument checks before any launch
+    bx = L.hbq_gemm_fp32_accum_batched_ex
+    assert bx(fake, fake, fake, 8, 256, 128, 256, 65536, 32768, 0, 128, 1024, None) == 1      # w_group 0
+    assert bx(fake, fake, fake, 8, 256, 128, 256, 65536, 32768, 4, 128, 64, None) == 1       # ldc < N
+    assert bx(fake, fake, fake, 8, 256, 128, 256, 65536, 32768, 4, 64, 1024, None) == 1      # outputs overlap
+    assert bx(fake, fake, fake, 8, 256, 128, 256, 100, 32768, 4, 128, 1024, None) == 1       # stride_a < M K
+    assert bx(fake, fake, fake, 0, 256, 128, 256, 65536, 32768, 4, 128, 1024, None) == 0     # no problems
+    assert L.hbq_gemm_fp32_accum_batched(fake, fake, fake, 2, 4, 8, 64, 256, 512, 16, None) == 1   # stride_c < M N
     # quantizer fused into the RMSNorm apply / SiLU product: only E2M2, one scheme, block 128
     q = [128, 2, 2, 5, 3, 32, 2, 2, 0, 0, 1]                  # HBQ-E act (SIG-1), compiled rule
 

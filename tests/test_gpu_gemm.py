@@ -333,6 +333,23 @@ def test_fp32_batched_equals_per_problem(gpu, Z, M, N, K):
         assert torch.equal(C[z].view(torch.int16), ref.view(torch.int16)), z
 
 
+def test_fp32_batched_gqa_rows_into_heads(gpu):
+    """hbq_gemm_fp32_accum_batched_ex as the decoder's P V uses it: 8 query heads over 2 kv
+    heads (W shared by groups of 4), each head's [T, d] output written at column h * d of
+    rows H * d long.  Every head gets the bits of the single GEMM on its own operands."""
+    from hbq_amd import _lib, blockquant_ext as ext
+    H, kvh, T, d = 8, 2, 256, 128
+    g = torch.Generator(device=gpu).manual_seed(78)
+    P = torch.rand(H, T, T, device=gpu, generator=g).half()
+    VT = (torch.randn(kvh, d, T, device=gpu, generator=g) * 0.5).half()
+    out = torch.full((T, H, d), 3.0, device=gpu, dtype=torch.float16)
+    _lib.check(_lib.lib().hbq_gemm_fp32_accum_batched_ex(_lib.ptr(P), _lib.ptr(VT), _lib.ptr(out), H, T, d, T, T * T,
+                                                         d * T, H // kvh, d, H * d, _lib.stream_of(P)))
+    for h in range(H):
+        ref = ext.gemm_fp32_accum_nk(P[h], VT[h // (H // kvh)])
+        assert torch.equal(out[:, h].view(torch.int16), ref.view(torch.int16)), h
+
+
 def test_fp32_batched_strides_beyond_one_problem(gpu):
     """Batch strides larger than one problem (problems inside wider buffers, as the ABI
     allows): each problem gets the bits of the single GEMM, and the gaps of C stay as

@@ -434,6 +434,24 @@ def test_silu_mul_quant_equals_two_passes(gpu, dt):
 
 
 @pytest.mark.gpu
+def test_attention_output_into_o_proj_layout(gpu):
+    """The P V product written straight into [b, T, H, d] (per query head, W shared by the
+    kv head's group) equals the kv-head-batched product transposed, bit for bit."""
+    m = LlamaForCausalLM(TINY).random_init_(seed=7).half().to(gpu)
+    a = m.layers[0].self_attn
+    g = torch.Generator(device=gpu).manual_seed(7)
+    b, T, d = 1, 256, TINY.head_dim
+    q = torch.randn(b, TINY.num_attention_heads, T, d, device=gpu, generator=g).half()
+    k = torch.randn(b, TINY.num_key_value_heads, T, d, device=gpu, generator=g).half()
+    vT = torch.randn(b, TINY.num_key_value_heads, d, T, device=gpu, generator=g).half()
+    with torch.no_grad():
+        ref, _ = a.manual_sdpa(q, k, None, vT=vT)
+        got, _ = a.manual_sdpa(q, k, None, vT=vT, out_bthd=True)
+    assert got.shape == (b, T, TINY.num_attention_heads, d) and got.is_contiguous()
+    assert torch.equal(got.view(torch.int16), ref.transpose(1, 2).contiguous().view(torch.int16))
+
+
+@pytest.mark.gpu
 def test_fused_input_quantizers_same_logits(gpu):
     """A prefill with the linears' input quantizers computed inside the norms and the SiLU
     product gives the logits of the separate passes bit for bit, with three fewer quantizer
