@@ -150,13 +150,24 @@ __global__ void build_lut_kernel(int slot, FastParams p) {
 template <class T>
 constexpr int fast_threads() { return T::dt == kF16 ? 512 : 256; }
 
+// Per-block magnitude rows.  One-scheme kernels with byte codes (M >= 2) keep the
+// negated magnitudes in the second half of each row: a level-word byte (level times
+// the entry size) plus L * sizeof(DT) addresses -d, so one LDS read of the selected
+// candidate returns the signed output.  Their rows are padded to start 8 banks apart
+// for the four blocks of a half-wave; the other kernels pad rows by one entry.
+template <class T, int M, int S>
+constexpr bool fast_signed_rows() { return S == 1 && M >= 2; }
+template <class T, int M, int S>
+constexpr int fast_row() {
+    return fast_signed_rows<T, M, S>() ? 2 * (1 << (M + 2)) + 32 / (int)sizeof(DTabT<T>) : (1 << (M + 2)) + 1;
+}
+
 // The in-place quantizer of causal attention weights (memory input, causal_t > 0) is
 // its own instantiation, so that the plain memory-input kernel can prefetch.
 constexpr int kSrcXCausal = 3;
 
 // Block 128 (8 lanes x 16 elements).  Per-wave magnitude tables, laid out
-// [scheme][candidate][block-in-wave][level] with rows padded by one entry so
-// that the eight blocks of a wave fall on different LDS banks.
+// [scheme][candidate][block-in-wave][row of fast_row() entries].
 template <class T, int M, int L2B, int S, int SRC = kSrcX>
 __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typename T::storage* __restrict__ x,
                                                             typename T::storage* __restrict__ y,
@@ -170,7 +181,8 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
     constexpr int bpw = 64 / lpb;
     constexpr int block = kV * lpb;
     constexpr int L = 1 << (M + 2);
-    constexpr int ROW = L + 1;                            // padded row (entries)
+    constexpr bool kSign = fast_signed_rows<T, M, S>();
+    constexpr int ROW = fast_row<T, M, S>();              // padded row (entries)
     constexpr int NSUBL = L2B <= kV ? kV / L2B : 1;
     constexpr int LPS = L2B <= kV ? 1 : L2B / kV;
     constexpr int SUBN = L2B <= kV ? L2B : kV;
@@ -354,7 +366,12 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
 #pragma unroll
                 for (int k = 0; k < CPL; ++k) {
                     const int c = li + k * lpb;
-                    if (c < L) dwave[((s * kFastJ + j) * bpw + bw) * ROW + c] = (DT)T::round(qs[s][j][k] * l1[s]);
+                    if (c < L) {
+                        const DT d = (DT)T::round(qs[s][j][k] * l1[s]);
+                        DT* r = dwave + ((s * kFastJ + j) * bpw + bw) * ROW;
+                        r[c] = d;
+                        if constexpr (kSign) r[L + c] = -d;
+                    }
                 }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -371,9 +388,12 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
         constexpr int KSH = T::dt == kBF16 ? 16 : 0;
         uint32_t tb[S][kV];
         int jsel[S][NSUBL];
+        bool slow[S];
+        float rl1v[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             const float rl1 = 1.0f / l1[s];
+            rl1v[s] = rl1;
             float qmin = xa[0] * rl1;
 #pragma unroll
             for (int i = 0; i < kV; ++i) {
@@ -381,7 +401,8 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
                 qmin = fminf(qmin, q);
                 tb[s][i] = key_of<T>(T::round(q));
             }
-            if (qmin < tiny) {   // quotients in T's subnormal range can be exact ties: divide
+            slow[s] = qmin < tiny;
+            if (slow[s]) {   // quotients in T's subnormal range can be exact ties: divide
 #pragma unroll
                 for (int i = 0; i < kV; ++i)
                     if (xa[i] * rl1 < tiny) tb[s][i] = key_of<T>(T::round(xa[i] / l1[s]));
@@ -439,77 +460,149 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
             }
         }
 
-        // the selected candidate of every scheme
-        float msel[S][kV];
-        uint32_t lsel[S][kV];
-#pragma unroll
-        for (int s = 0; s < S; ++s)
-#pragma unroll
-            for (int i = 0; i < kV; ++i) {
-                const int j = jsel[s][i / SUBN];
-                const uint32_t off8 = (ent[s][i] >> (8 * j)) & 0xffu;
-                lsel[s][i] = off8 / sizeof(DT);
-                const char* a = drow0 + ((s * kFastJ + j) * bpw) * ROW * sizeof(DT) + off8;
-                msel[s][i] = (float)*reinterpret_cast<const DT*>(a);
-            }
         int sstar = 0;
-        if constexpr (S == 2) {
-            float sq0[kV], sq1[kV];
+        if constexpr (kSign) {
+            // The selected candidate's level-word bytes (level times the entry size) of 4
+            // elements in one register (v_perm_b32 picks byte j of two words at a time), and
+            // the signs of x as byte masks (v_perm selectors 8-11 replicate bits 15, 31, 47
+            // and 63 of its two input words: the signs of 4 packed 16-bit elements).
+            constexpr int ES = (int)sizeof(DT);
+            constexpr uint32_t kNeg = (uint32_t)(L * ES) * 0x01010101u;     // byte offset of -d in a row
+            constexpr uint32_t kCodeSign = (1u << (M + 2)) * 0x01010101u;   // sign bit of a byte code
+            uint32_t pb[4], xm[4];
 #pragma unroll
-            for (int i = 0; i < kV; i += 2) {
-                float a0, a1, b0, b1;
-                round2<T>(xa[i] - msel[0][i], xa[i + 1] - msel[0][i + 1], a0, a1);
-                round2<T>(a0 * a0, a1 * a1, sq0[i], sq0[i + 1]);
-                round2<T>(xa[i] - msel[S - 1][i], xa[i + 1] - msel[S - 1][i + 1], b0, b1);
-                round2<T>(b0 * b0, b1 * b1, sq1[i], sq1[i + 1]);
+            for (int g = 0; g < 4; ++g) {
+                const uint32_t j = (uint32_t)jsel[0][(4 * g) / SUBN];
+                const uint32_t sel = j | ((j + 4u) << 8) | 0x0c0c0000u;   // byte j of the low word, then of the high word
+                const uint32_t lo = __builtin_amdgcn_perm(ent[0][4 * g + 1], ent[0][4 * g], sel);
+                const uint32_t hi = __builtin_amdgcn_perm(ent[0][4 * g + 3], ent[0][4 * g + 2], sel);
+                pb[g] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+                xm[g] = __builtin_amdgcn_perm(w[2 * g + 1], w[2 * g], 0x0b0a0908u);
             }
-            const float s0 = T::round(block_row_sum(sq0, li, lpb, lane_base));
-            const float s1 = T::round(block_row_sum(sq1, li, lpb, lane_base));
-            sstar = better(s1, s0) ? 1 : 0;
-        }
-
-        float out[kV];
-        uint32_t cout[kV];
-        uint32_t zsel[NSUBL];
+            // The output keeps the sign of x unless u = R_T(t / l2_j) is 0 (then +0 and a
+            // positive code), which needs t < z_j: a quotient below T's normal range, which
+            // the check above flags (x = +-0 included).
+            if (slow[0]) {
 #pragma unroll
-        for (int sb = 0; sb < NSUBL; ++sb) {
-            const int s = (S == 2 && sstar) ? S - 1 : 0;
-            const int j = jsel[s][sb];
-            float zz = z[s][0];
+                for (int i = 0; i < kV; ++i) {
+                    const int j = jsel[0][i / SUBN];
+                    float zz = z[0][0];
 #pragma unroll
-            for (int jj = 1; jj < kFastJ; ++jj) zz = j == jj ? z[s][jj] : zz;
-            zsel[sb] = key_of<T>(zz);
-        }
+                    for (int jj = 1; jj < kFastJ; ++jj) zz = j == jj ? z[0][jj] : zz;
+                    // recomputed, not taken from the keys above: those die after the table index
+                    uint32_t wv = w[i / 2];
+                    asm("" : "+v"(wv));
+                    const float a = fabsf(T::load((typename T::storage)(wv >> (16 * (i % 2)))));
+                    const float q = a * rl1v[0];
+                    const float t = q < tiny ? T::round(a / l1[0]) : T::round(q);
+                    if (!(key_of<T>(t) >= key_of<T>(zz))) xm[i / 4] &= ~(0xffu << (8 * (i % 4)));
+                }
+            }
+            // signed magnitudes: row of the selected candidate, byte offset plus L * ES if negative
+            const char* rsel[NSUBL];
 #pragma unroll
-        for (int i = 0; i < kV; ++i) {
-            const bool s1 = S == 2 && sstar;
-            const uint32_t t = s1 ? tb[S - 1][i] : tb[0][i];
-            const bool neg = (f2bits(xv[i]) >> 31) && t >= zsel[i / SUBN];
-            const float m = s1 ? msel[S - 1][i] : msel[0][i];
-            out[i] = neg ? -m : m;
-            const uint32_t lev = s1 ? lsel[S - 1][i] : lsel[0][i];
-            cout[i] = lev | ((neg ? 1u : 0u) << (M + 2));
-        }
-        if (valid) {
-            store16<T>(y + off, out);
-            if (codes) {
-                if constexpr (M == 1) {
-                    uint32_t w0 = 0, w1 = 0;
+            for (int sb = 0; sb < NSUBL; ++sb) rsel[sb] = drow0 + (jsel[0][sb] * bpw) * ROW * ES;
+            uint32_t ps[4];
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        w0 |= (cout[i] & 0xfu) << (4 * i);
-                        w1 |= (cout[8 + i] & 0xfu) << (4 * i);
-                    }
-                    *reinterpret_cast<uint2*>(codes + off / 2) = make_uint2(w0, w1);
-                } else {
+            for (int g = 0; g < 4; ++g) ps[g] = (xm[g] & kNeg) | pb[g];
+            DT m[kV];
+#pragma unroll
+            for (int i = 0; i < kV; ++i)
+                m[i] = *reinterpret_cast<const DT*>(rsel[i / SUBN] + ((ps[i / 4] >> (8 * (i % 4))) & 0xffu));
+            uint32_t yw[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                if constexpr (T::dt == kBF16)   // the high halves: the values are bf16 already
+                    yw[k] = __builtin_amdgcn_perm(f2bits((float)m[2 * k + 1]), f2bits((float)m[2 * k]), 0x07060302u);
+                else
+                    yw[k] = (uint32_t)__builtin_bit_cast(uint16_t, m[2 * k]) |
+                            ((uint32_t)__builtin_bit_cast(uint16_t, m[2 * k + 1]) << 16);
+            }
+            if (valid) {
+                u32x4_t* q = reinterpret_cast<u32x4_t*>(y + off);
+                __builtin_nontemporal_store((u32x4_t){yw[0], yw[1], yw[2], yw[3]}, q);
+                __builtin_nontemporal_store((u32x4_t){yw[4], yw[5], yw[6], yw[7]}, q + 1);
+                if (codes) {   // byte codes: level | sign << (M + 2)
                     uint32_t cw[4];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        cw[i] = (cout[4 * i] & 0xffu) | ((cout[4 * i + 1] & 0xffu) << 8) |
-                                ((cout[4 * i + 2] & 0xffu) << 16) | ((cout[4 * i + 3] & 0xffu) << 24);
+                    for (int g = 0; g < 4; ++g) cw[g] = (pb[g] / (uint32_t)ES) | (xm[g] & kCodeSign);
                     *reinterpret_cast<uint4*>(codes + off) = make_uint4(cw[0], cw[1], cw[2], cw[3]);
                 }
             }
+        } else {
+            // the selected candidate of every scheme
+            float msel[S][kV];
+            uint32_t lsel[S][kV];
+    #pragma unroll
+            for (int s = 0; s < S; ++s)
+    #pragma unroll
+                for (int i = 0; i < kV; ++i) {
+                    const int j = jsel[s][i / SUBN];
+                    const uint32_t off8 = (ent[s][i] >> (8 * j)) & 0xffu;
+                    lsel[s][i] = off8 / sizeof(DT);
+                    const char* a = drow0 + ((s * kFastJ + j) * bpw) * ROW * sizeof(DT) + off8;
+                    msel[s][i] = (float)*reinterpret_cast<const DT*>(a);
+                }
+            if constexpr (S == 2) {
+                float sq0[kV], sq1[kV];
+    #pragma unroll
+                for (int i = 0; i < kV; i += 2) {
+                    float a0, a1, b0, b1;
+                    round2<T>(xa[i] - msel[0][i], xa[i + 1] - msel[0][i + 1], a0, a1);
+                    round2<T>(a0 * a0, a1 * a1, sq0[i], sq0[i + 1]);
+                    round2<T>(xa[i] - msel[S - 1][i], xa[i + 1] - msel[S - 1][i + 1], b0, b1);
+                    round2<T>(b0 * b0, b1 * b1, sq1[i], sq1[i + 1]);
+                }
+                const float s0 = T::round(block_row_sum(sq0, li, lpb, lane_base));
+                const float s1 = T::round(block_row_sum(sq1, li, lpb, lane_base));
+                sstar = better(s1, s0) ? 1 : 0;
+            }
+
+            float out[kV];
+            uint32_t cout[kV];
+            uint32_t zsel[NSUBL];
+    #pragma unroll
+            for (int sb = 0; sb < NSUBL; ++sb) {
+                const int s = (S == 2 && sstar) ? S - 1 : 0;
+                const int j = jsel[s][sb];
+                float zz = z[s][0];
+    #pragma unroll
+                for (int jj = 1; jj < kFastJ; ++jj) zz = j == jj ? z[s][jj] : zz;
+                zsel[sb] = key_of<T>(zz);
+            }
+    #pragma unroll
+            for (int i = 0; i < kV; ++i) {
+                const bool s1 = S == 2 && sstar;
+                const uint32_t t = s1 ? tb[S - 1][i] : tb[0][i];
+                const bool neg = (f2bits(xv[i]) >> 31) && t >= zsel[i / SUBN];
+                const float m = s1 ? msel[S - 1][i] : msel[0][i];
+                out[i] = neg ? -m : m;
+                const uint32_t lev = s1 ? lsel[S - 1][i] : lsel[0][i];
+                cout[i] = lev | ((neg ? 1u : 0u) << (M + 2));
+            }
+            if (valid) {
+                store16<T>(y + off, out);
+                if (codes) {
+                    if constexpr (M == 1) {
+                        uint32_t w0 = 0, w1 = 0;
+    #pragma unroll
+                        for (int i = 0; i < 8; ++i) {
+                            w0 |= (cout[i] & 0xfu) << (4 * i);
+                            w1 |= (cout[8 + i] & 0xfu) << (4 * i);
+                        }
+                        *reinterpret_cast<uint2*>(codes + off / 2) = make_uint2(w0, w1);
+                    } else {
+                        uint32_t cw[4];
+    #pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            cw[i] = (cout[4 * i] & 0xffu) | ((cout[4 * i + 1] & 0xffu) << 8) |
+                                    ((cout[4 * i + 2] & 0xffu) << 16) | ((cout[4 * i + 3] & 0xffu) << 24);
+                        *reinterpret_cast<uint4*>(codes + off) = make_uint4(cw[0], cw[1], cw[2], cw[3]);
+                    }
+                }
+            }
+        }
+        if (valid) {
             if (li == 0) {
                 if (l1_out) l1_out[gb] = T::store((S == 2 && sstar) ? l1[S - 1] : l1[0]);
                 if (sch_out) sch_out[gb] = (uint8_t)sstar;
@@ -571,7 +664,7 @@ int launch_fast(const void* x, void* y, void* l1, void* l2i, void* sch, void* co
     constexpr int NTH = fast_threads<T>();
     using St = typename T::storage;
     const size_t lds = (size_t)S * (p.n + 2) * 4 +
-                       (size_t)(NTH >> lpb_log2) * S * kFastJ * ((1 << (M + 2)) + 1) * sizeof(DTabT<T>);
+                       (size_t)(NTH >> lpb_log2) * S * kFastJ * fast_row<T, M, S>() * sizeof(DTabT<T>);
     if (lds > 160 * 1024) return 0;
     if constexpr (SRC == kSrcX) {
         if (causal_t) return launch_fast<T, M, L2B, S, kSrcXCausal>(x, y, l1, l2i, sch, codes, nb, causal_t, slot, p, dev, st);

@@ -25,6 +25,9 @@ HBQCFG = {
     "hbq_kv4": dict(ebit=2, mbit=1, l2_block_size=8, l2_sc_bit=2, l2_scheme="SIG-1"),
     "hbq_a_wgt_ceil": dict(ebit=2, mbit=1, l2_block_size=8, l2_sc_bit=2, l2_scheme="Mix", use_ceil=True),
     "hbq_pot": dict(ebit=2, mbit=1, l2_block_size=4, l2_sc_bit=1, l2_scheme="PoT"),
+    # no reference fixtures for these two: checked against the oracle and the generic kernel
+    "hbq_m3": dict(ebit=2, mbit=3, l2_block_size=8, l2_sc_bit=2, l2_scheme="SIG-1"),
+    "hbq_l16": dict(ebit=2, mbit=2, l2_block_size=16, l2_sc_bit=2, l2_scheme="FP-1"),
 }
 
 
@@ -104,7 +107,7 @@ def test_mxfp_bf16_raises(gpu):
         _mx(MXCFG["mxfp4"]).q(torch.zeros(4, 32, dtype=torch.bfloat16, device=gpu))
 
 
-@pytest.mark.parametrize("name", list(HBQCFG))
+@pytest.mark.parametrize("name", [n for n in HBQCFG if n not in ("hbq_m3", "hbq_l16")])
 @pytest.mark.parametrize("inp", ["f16", "f16w", "bf16"])
 @pytest.mark.parametrize("uqk", [False, True])
 def test_hbq_golden(gpu, golden_hbq, golden_extra, golden_compiled, name, inp, uqk):
@@ -154,7 +157,8 @@ def test_hbq_golden_ragged(gpu, golden_hbq):
 
 
 def _edge_rows(x):
-    """Overwrite a few rows with zeros, +-inf, NaN, huge and subnormal values."""
+    """Overwrite a few rows with zeros, +-inf, NaN, huge and subnormal values, negative zeros,
+    and blocks whose small elements give u = R(t / l2) = 0 (the output is +0 whatever the sign)."""
     x = x.clone()
     x[0] = 0
     x[1, ::7] = float("inf")
@@ -162,6 +166,10 @@ def _edge_rows(x):
     x[3, 3::11] = -float("inf")
     x[4] = x[4] * 1e-6
     x[5] = x[5].sign() * 60000
+    x[6, ::2] = -0.0
+    tiny, big = (6e-8, 6e4) if x.dtype == torch.float16 else (1e-38, 1e5)
+    x[7] = x[7].sign() * tiny
+    x[7, ::128] = big
     return x
 
 
@@ -269,7 +277,8 @@ def test_hbq_3d_input(gpu, oracle):
     assert mismatches(to_bits(y.view(-1, 256)), ref["y"], "f16") == 0
 
 
-@pytest.mark.parametrize("name", ["hbq_a_act", "hbq_a_wgt", "hbq_e_act", "hbq_e_wgt", "hbq_kv4", "hbq_a_wgt_ceil"])
+@pytest.mark.parametrize("name", ["hbq_a_act", "hbq_a_wgt", "hbq_e_act", "hbq_e_wgt", "hbq_kv4", "hbq_a_wgt_ceil",
+                                  "hbq_m3", "hbq_l16"])
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("uqk", [True, False])
 def test_hbq_table_kernel_equals_generic(gpu, name, dt, uqk):
