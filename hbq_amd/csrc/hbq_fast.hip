@@ -46,6 +46,9 @@ static __device__ float g_lut_z[kLutSlots][2 * kFastJ];
 // per slot: R_T(level value * l2[j][s]) for every level (block independent)
 static __device__ float g_lut_qs[kLutSlots][2][kFastJ][32];
 static __device__ int g_lut_status[kLutSlots];
+// 1 when v_rcp_f32 returns the correctly rounded 1 / l1 for every E5M3 L1 scale the
+// table kernel can produce (2^e (1 + m / 8), e in [-14, 15]); set by the table build
+static __device__ int g_rcp_exact;
 
 struct FastParams {
     int S, J, L;               // schemes, candidates, levels (2^(m+2))
@@ -141,6 +144,14 @@ __global__ void build_lut_kernel(int slot, FastParams p) {
                 g_lut_z[slot][s * kFastJ + j] = z;
             }
         g_lut_status[slot] = status;
+        int exact = 1;
+        for (int e = -14; e <= 15; ++e)
+            for (int m = 0; m < 8; ++m) {
+                float v = ldexpf(1.0f + 0.125f * (float)m, e);
+                asm volatile("" : "+v"(v));   // the hardware's reciprocal, not a folded constant
+                if (__builtin_amdgcn_rcpf(v) != 1.0f / v) exact = 0;
+            }
+        g_rcp_exact = exact;
     }
 }
 
@@ -217,6 +228,7 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
     const char* drow0 = reinterpret_cast<const char*>(dwave + bw * ROW);
     const int64_t ntiles = (nb + blocks_per_wg - 1) / blocks_per_wg;
     const float tiny = T::dt == kF16 ? 6.103515625e-05f : 1.17549435e-38f;
+    const bool rcp_exact = __builtin_amdgcn_readfirstlane(g_rcp_exact) != 0;
 
     // causal_t > 0 (kSrcXCausal only): nb blocks of [mats, t, t] attention weights whose
     // blocks above the diagonal are zero and stay as they are (y == x): each wave takes one
@@ -267,8 +279,10 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
         // load 16 elements; the block max of |x| over the raw 16-bit patterns
         uint32_t w[8];
         if constexpr (kPrefetch) {
-            w[0] = valid ? pf0.x : 0u; w[1] = valid ? pf0.y : 0u; w[2] = valid ? pf0.z : 0u; w[3] = valid ? pf0.w : 0u;
-            w[4] = valid ? pf1.x : 0u; w[5] = valid ? pf1.y : 0u; w[6] = valid ? pf1.z : 0u; w[7] = valid ? pf1.w : 0u;
+            // a lane past the end keeps the data it loaded: its block is never stored and
+            // its lanes read only their own block's table rows
+            w[0] = pf0.x; w[1] = pf0.y; w[2] = pf0.z; w[3] = pf0.w;
+            w[4] = pf1.x; w[5] = pf1.y; w[6] = pf1.z; w[7] = pf1.w;
             prefetch(tile + stride, valid ? gb : 0);
         } else if (valid) {
             if constexpr (kMem) {
@@ -323,9 +337,9 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
         for (int s = 0; s < S; ++s) {
             // R_T(amax * R32(1/em)) = R_T(amax / em) for quotients in T's normal range;
             // below it both clamp to 2^-14 (exhaustive CPU check over every T value)
-            float sc = T::round(amax * p.rem[s]);
-            sc = sc < 6.103515625e-05f ? 6.103515625e-05f : (sc > 61440.f ? 61440.f : sc);
-            l1[s] = sc != sc ? sc : e5m3_scale<T>(sc, p.use_ceil);
+            const float sr = T::round(amax * p.rem[s]);
+            const float sc = __builtin_amdgcn_fmed3f(sr, 6.103515625e-05f, 61440.f);   // (v_med3 maps NaN to a bound)
+            l1[s] = sr != sr ? sr : e5m3_scale<T>(sc, p.use_ceil);
         }
 
         // every block of this wave all zero (the masked half of causal attention weights):
@@ -392,7 +406,13 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
         float rl1v[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-            const float rl1 = 1.0f / l1[s];
+            float rl1;   // l1 is an E5M3 value (or NaN): one v_rcp_f32 where the table build found it exact
+            if (rcp_exact) {
+                rl1 = __builtin_amdgcn_rcpf(l1[s]);
+            } else {
+                asm volatile("");   // a real (uniform) branch: keeps the division from being speculated
+                rl1 = 1.0f / l1[s];
+            }
             rl1v[s] = rl1;
             float qmin = xa[0] * rl1;
 #pragma unroll
