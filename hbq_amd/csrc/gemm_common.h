@@ -98,24 +98,17 @@ __device__ __forceinline__ float xlane32_max(float v) {
     return fmaxf(v, fmaxf(a, b));
 }
 
-// R16(t0 - M) and R16(t1 - M) packed in one register, each by one v_fma_mix
-// (t * 1 - M with a single rounding of the exact difference).  The first
-// instruction writes only the low half, the second only the high half, so the
-// register needs no prior value.
-__device__ __forceinline__ h2_t sub_pair(float t0, float t1, float M) {
-    h2_t h;
-    asm("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,0]" : "=v"(h) : "v"(t0), "v"(M));
-    asm("v_fma_mixhi_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,0]" : "+v"(h) : "v"(t1), "v"(M));
-    return h;
-}
-
-// R16(t0 - M0) and R16(t1 - M1) packed in one register (two v_fma_mix)
+// R16(t0 - M0) and R16(t1 - M1) packed in one register.  The differences are exact
+// in fp32 (t and M lie within a factor of 2), so two v_sub_f32 and one
+// v_cvt_pk_f16_f32 round each once.  (A v_fma_mix per value does the same in one
+// instruction, but issues at half the rate of a conversion and a quarter of a
+// subtraction; the barriers keep the compiler from forming it.)
 __device__ __forceinline__ h2_t sub_pair2(float t0, float M0, float t1, float M1) {
-    h2_t h;
-    asm("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,0]" : "=v"(h) : "v"(t0), "v"(M0));
-    asm("v_fma_mixhi_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,0]" : "+v"(h) : "v"(t1), "v"(M1));
-    return h;
+    float d0 = t0 - M0, d1 = t1 - M1;
+    asm("" : "+v"(d0), "+v"(d1));
+    return cvt2(d0, d1);
 }
+__device__ __forceinline__ h2_t sub_pair(float t0, float t1, float M) { return sub_pair2(t0, M, t1, M); }
 
 __device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
 
@@ -135,8 +128,8 @@ __device__ __forceinline__ float e3m4_magic(float P, uint32_t msub) {
 // mxint8: with the group max mx normal, s = 2^(ilogb(mx) - 6), |P| / s < 128,
 // and rne(P / s) * s = (P + M) - M with M = 1.5 * 2^23 * s: the add rounds P
 // to the nearest (even) multiple of ulp(M) = s and the subtraction is exact.
-// (fp16 products bound |P| by 2^39 and nonzero |P| below by 2^-48.)  The
-// subtraction and the rounding to fp16 share one v_fma_mix.  NaN partials stay
+// (fp16 products bound |P| by 2^39 and nonzero |P| below by 2^-48.)  A pair's
+// two exact differences round to fp16 in one v_cvt_pk_f16_f32.  NaN partials stay
 // NaN, as in the reference.  Only a group whose max has a mantissa of at least
 // 1 + 127/128 (mx / s >= 127.5) can round to +-128 s; when a lane of the wave
 // holds such a group the block also clamps, on the fp16 values: R16 is
