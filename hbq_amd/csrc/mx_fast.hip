@@ -88,6 +88,8 @@ __global__ void build_mx_lut_kernel(int slot, int n, uint32_t lo_bits, int fused
     }
 }
 
+typedef _Float16 mx_h2_t __attribute__((ext_vector_type(2)));
+
 // R16(|lo half of h| * f) into the low half of the result, one v_fma_mix (a single rounding)
 __device__ __forceinline__ uint32_t mix_lo(uint32_t h, float f) {
     uint32_t d;
@@ -207,6 +209,7 @@ __global__ __launch_bounds__(kMxThreads) void mx_fast_kernel(const uint16_t* __r
 
         uint32_t y2[2][4];
         uint32_t cout[2][8];
+        const mx_h2_t s2h[2] = {(mx_h2_t){(_Float16)s[0], (_Float16)s[0]}, (mx_h2_t){(_Float16)s[1], (_Float16)s[1]}};
         if (__builtin_expect(__builtin_amdgcn_ballot_w64(special) != 0, 0)) {
             // a NaN in the wave's tile, or a scale that rounds to 0 or inf in fp16 (an
             // 8-bit scale exponent): the generic element path
@@ -264,8 +267,9 @@ __global__ __launch_bounds__(kMxThreads) void mx_fast_kernel(const uint16_t* __r
                     }
                     // the two magnitudes (high halves of the words) as one packed pair
                     const uint32_t q2 = __builtin_amdgcn_perm(e2[1], e2[0], 0x07060302u);
-                    uint32_t o2 = mix_lo(q2, s[h]);   // R16(q * s): exact product
-                    mix_hi(o2, q2, s[h]);
+                    // R16(q * s) of both: s is an fp16 value here, so v_pk_mul_f16 rounds the
+                    // exact products once
+                    const uint32_t o2 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(mx_h2_t, q2) * s2h[h]);
                     // the sign of x unless u is +-0 (the reference's u == 0 gives +0 and code 0):
                     // bit 15 of each half of u2 + 0x7fff7fff is set iff that half is nonzero
                     // (u <= 0x7c00, so no carry crosses the halves)
