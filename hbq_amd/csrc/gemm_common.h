@@ -137,10 +137,13 @@ __device__ __forceinline__ float e3m4_magic(float P, uint32_t msub) {
 // gives R16(clamp(q)), and v_pk_minimum3/maximum3 propagate NaN.  An all-zero
 // group (mx = 0) gets M = 1.5 * 2^-110 from the same bit arithmetic, which
 // turns every +-0 into +0 (the sign of a zero addend cannot change an
-// accumulator that starts at +0 and only adds fp16 values).  When a lane holds
-// a group with an infinite max (every output NaN, as P / inf * inf) or a
-// nonzero max outside [2^-100, 2^110), the whole wave takes the exact formula.
-// The branches depend on wave-wide ballots, so they are scalar branches.
+// accumulator that starts at +0 and only adds fp16 values).  The magic
+// constants stay normal floats for a max in [2^-100, 2^110); with fp16 operands
+// a nonzero partial is at least 2^-48 (a multiple of the smallest product) and a
+// finite one below 2^39, so only an infinite max (every output NaN, as
+// P / inf * inf) leaves that range: when a lane holds one, the whole wave takes
+// the exact formula.  The branches depend on wave-wide ballots, so they are
+// scalar branches.
 template <int MODE, int GN>
 __device__ __forceinline__ void fold_block_impl(const f16v& acc, h2_t* H) {
     if constexpr (MODE == kGrouped) {
@@ -158,7 +161,7 @@ __device__ __forceinline__ void fold_block_impl(const f16v& acc, h2_t* H) {
             for (int r = g * RPG; r < (g + 1) * RPG; ++r) mx = fmaxf(mx, fabsf(acc[r]));
             if constexpr (GN >= 8) mx = xlane32_max(mx);
             mxg[g] = mx;
-            special |= (mx >= 0x1p110f) | ((mx < 0x1p-100f) & (mx != 0.f));
+            special |= mx >= 0x1p110f;   // a nonzero max is at least 2^-48 (fp16 operands)
             top |= (__builtin_bit_cast(uint32_t, mx) & 0x7fffffu) >= 0x7f0000u;
         }
         if constexpr (MODE == kInt8) {
@@ -203,14 +206,14 @@ __device__ __forceinline__ void fold_block_impl(const f16v& acc, h2_t* H) {
                 for (int p = 0; p < 8; ++p) H[p] = H[p] + cvt2(q[2 * p], q[2 * p + 1]);
             }
         } else {
-            // mxfp8: the fast path needs the group max in [2^-100, 2^100) (or zero), where
-            // the magic constants stay normal floats; a max with a mantissa of at least
+            // mxfp8: the fast path needs the group max below 2^100 (a nonzero max is at
+            // least 2^-48), where the magic constants stay normal floats; a max with a mantissa of at least
             // 1 + 31/32 (mx / s >= 15.75) can round to 16 s, which the clamp to
             // R16(15.5 s) turns into the reference's 15.5 s
             bool special8 = false, top8 = false;
 #pragma unroll
             for (int g = 0; g < NG; ++g) {
-                special8 |= (mxg[g] >= 0x1p100f) | ((mxg[g] < 0x1p-100f) & (mxg[g] != 0.f));
+                special8 |= mxg[g] >= 0x1p100f;
                 top8 |= (__builtin_bit_cast(uint32_t, mxg[g]) & 0x7fffffu) >= 0x7c0000u;
             }
             if (__builtin_expect(!wave_any(special8), 1)) {
