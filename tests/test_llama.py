@@ -400,6 +400,14 @@ def test_rms_apply_quant_equals_two_passes(gpu, dt):
         x[4, ::7] *= 80.0                                   # outlier channels
         res[2, 5] = float("inf")
         res[3, 7] = float("nan")
+        # a huge value per block and tiny ones whose quotients underflow (u = 0: +0 whatever
+        # the sign), and a row of negative zeros
+        big, tiny = (6e4, 6e-8) if dt == torch.float16 else (1e30, 1e-30)
+        x[5, :] = tiny * torch.sign(x[5, :])
+        x[5, ::128] = big
+        res[5, :] = 0.0
+        x[6, :] = -0.0
+        res[6, :] = -0.0
         for kw in FUSED_QZ:
             qz = _fused_qz(kw)
             with torch.no_grad():
@@ -418,13 +426,20 @@ def test_rms_apply_quant_equals_two_passes(gpu, dt):
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
 def test_silu_mul_quant_equals_two_passes(gpu, dt):
     """silu(gate) * up with the input quantizer in the same pass gives aq.q(silu_mul(gate,
-    up)) bit for bit: every 16-bit pattern of the gate, and a [37, 14336] MLP-shaped input."""
+    up)) bit for bit: every 16-bit pattern of the gate, a [37, 14336] MLP-shaped input, and
+    blocks whose tiny products quantize to u = 0 next to a huge one."""
     from hbq_amd.llama import silu_mul, silu_mul_quant
     g = torch.Generator(device=gpu).manual_seed(32)
     gate_all = torch.arange(-32768, 32768, dtype=torch.int32, device=gpu).to(torch.int16).view(dt).view(512, 128)
+    # blocks of one huge product and tiny ones of either sign, whose quotients underflow
+    big, tiny = (6e4, 6e-8) if dt == torch.float16 else (1e30, 1e-30)
+    mix = torch.full((64, 1024), -tiny, device=gpu).to(dt)
+    mix[:, 1::3] = tiny
+    mix[:, ::128] = big
     cases = [(gate_all, (torch.randn(512, 128, device=gpu, generator=g) * 4).to(dt)),
              ((torch.randn(37, 14336, device=gpu, generator=g) * 2).to(dt),
-              (torch.randn(37, 14336, device=gpu, generator=g)).to(dt))]
+              (torch.randn(37, 14336, device=gpu, generator=g)).to(dt)),
+             (mix, torch.ones(64, 1024, device=gpu).to(dt))]
     for gate, up in cases:
         for kw in FUSED_QZ:
             qz = _fused_qz(kw)
