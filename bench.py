@@ -273,6 +273,31 @@ def packed_extra(dev, iters=20):
     return out
 
 
+def vllm_extra(dev, iters=20):
+    """The vLLM plugin's linear method (default NVFP4 config) on a 4096 -> 4096 projection:
+    weight quantization after loading, and apply() (activation quantizer + matmul) for a
+    decode-sized (16 tokens) and a prefill-sized (2048 tokens) input."""
+    from hbq_amd import vllm_plugin as vp
+    g = torch.Generator(device=dev).manual_seed(15)
+    cfg = vp.default_nvfp4_config()
+    lin = torch.nn.Linear(4096, 4096, bias=False).to(dev).half()
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(4096, 4096, device=dev, generator=g) * 0.02)
+    m = vp.HBQNVFP4Config(cfg).get_quant_method(lin, "model.layers.0.self_attn.o_proj")
+    w0 = lin.weight.detach().clone()
+    for _ in range(2):   # the first call builds the quantizer's level table
+        vp.quantize_weight_in_chunks(w0, m.wgt_q, 1024)
+    t_w = HipTimer().run(lambda: vp.quantize_weight_in_chunks(w0, m.wgt_q, 1024), 5)
+    m.process_weights_after_loading(lin)
+    out = {"vllm_nvfp4_weight_quant_us": round(t_w * 1e6, 1)}
+    for tok in (16, 2048):
+        x = torch.randn(tok, 4096, device=dev, generator=g).half()
+        for _ in range(3):
+            m.apply(lin, x)
+        out[f"vllm_nvfp4_apply_{tok}tok_us"] = round(HipTimer().run(lambda: m.apply(lin, x), iters) * 1e6, 1)
+    return out
+
+
 def prefill_extra(dev, T=2048, iters=3):
     """one prefill of T tokens through Llama-3-8B (32 layers, random N(0, 0.02)
     weights, fp16) with the HBQ-A + KV quantization points; weights quantized once beforehand.
@@ -525,6 +550,7 @@ def main():
             extra.update(quant_config_extra(dev))
             extra.update(config0_extra(dev))
             extra.update(gemm_extra(dev))
+            extra.update(vllm_extra(dev))
             extra.update(prefill_extra(dev))
     # device-to-device copy of the same tensor: the measured bandwidth ceiling, and the
     # known-size kernel that scales the HBM byte counters
