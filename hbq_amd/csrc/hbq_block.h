@@ -59,7 +59,11 @@ __device__ __forceinline__ void hbq_block(const float* xv, int li, int lpb, int 
                 float acc = 0.f;
 #pragma unroll
                 for (int i = 0; i < n; ++i) acc += sqj[sb * n + i];
-                if (LPS > 1) {
+                if constexpr (LPS == 2) {
+                    // a lane pair: DPP swap within the pair (quad_perm 1,0,3,2) and one
+                    // add, the same bits in both lanes since a + b == b + a
+                    acc = acc + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(acc), 0xb1, 0xf, 0xf, true));
+                } else if constexpr (LPS > 1) {
                     // sub-block spans LPS lanes: fold their 16-term sums in lane order
                     const int first = lane - (li % LPS);
                     float tot = __shfl(acc, first, 64);

@@ -465,7 +465,14 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
                             acc += q1;
                         }
                     }
-                    if (LPS > 1) {
+                    if constexpr (LPS == 2) {
+                        // the lane pair's two partial sums: a DPP swap within the pair
+                        // (quad_perm 1,0,3,2) and one add, the same bits in both lanes since
+                        // a + b == b + a
+                        const float o = __int_as_float(
+                            __builtin_amdgcn_mov_dpp(__float_as_int(acc), 0xb1, 0xf, 0xf, true));
+                        acc = acc + o;
+                    } else if constexpr (LPS > 1) {
                         const int first = lane - (li % LPS);
                         float tot = __shfl(acc, first, 64);
                         for (int k2 = 1; k2 < LPS; ++k2) tot += __shfl(acc, first + k2, 64);
