@@ -161,16 +161,13 @@ __global__ void build_lut_kernel(int slot, FastParams p) {
 template <class T>
 constexpr int fast_threads() { return T::dt == kF16 ? 512 : 256; }
 
-// Per-block magnitude rows.  One-scheme kernels with byte codes (M >= 2) keep the
-// negated magnitudes in the second half of each row: a level-word byte (level times
-// the entry size) plus L * sizeof(DT) addresses -d, so one LDS read of the selected
-// candidate returns the signed output.  Their rows are padded to start 8 banks apart
-// for the four blocks of a half-wave; the other kernels pad rows by one entry.
-template <class T, int M, int S>
-constexpr bool fast_signed_rows() { return S == 1 && M >= 2; }
-template <class T, int M, int S>
+// Per-block magnitude rows.  The negated magnitudes fill the second half of each
+// row: a level-word byte (level times the entry size) plus L * sizeof(DT) addresses
+// -d, so one LDS read of the selected candidate returns the signed output.  Rows are
+// padded to start 8 banks apart for the four blocks of a half-wave.
+template <class T, int M>
 constexpr int fast_row() {
-    return fast_signed_rows<T, M, S>() ? 2 * (1 << (M + 2)) + 32 / (int)sizeof(DTabT<T>) : (1 << (M + 2)) + 1;
+    return 2 * (1 << (M + 2)) + 32 / (int)sizeof(DTabT<T>);
 }
 
 // The in-place quantizer of causal attention weights (memory input, causal_t > 0) is
@@ -192,8 +189,7 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
     constexpr int bpw = 64 / lpb;
     constexpr int block = kV * lpb;
     constexpr int L = 1 << (M + 2);
-    constexpr bool kSign = fast_signed_rows<T, M, S>();
-    constexpr int ROW = fast_row<T, M, S>();              // padded row (entries)
+    constexpr int ROW = fast_row<T, M>();              // padded row (entries)
     constexpr int NSUBL = L2B <= kV ? kV / L2B : 1;
     constexpr int LPS = L2B <= kV ? 1 : L2B / kV;
     constexpr int SUBN = L2B <= kV ? L2B : kV;
@@ -323,13 +319,11 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
         uint32_t m2 = mp.x > mp.y ? (uint32_t)mp.x : (uint32_t)mp.y;
         m2 = max8_dpp(m2);
         const float amax = T::load((typename T::storage)m2);
-        float xv[kV], xa[kV];
+        float xa[kV];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            xv[2 * i] = T::load((typename T::storage)(w[i] & 0xffffu));
-            xv[2 * i + 1] = T::load((typename T::storage)(w[i] >> 16));
-            xa[2 * i] = fabsf(xv[2 * i]);
-            xa[2 * i + 1] = fabsf(xv[2 * i + 1]);
+            xa[2 * i] = fabsf(T::load((typename T::storage)(w[i] & 0xffffu)));
+            xa[2 * i + 1] = fabsf(T::load((typename T::storage)(w[i] >> 16)));
         }
 
         float l1[S];
@@ -384,7 +378,7 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
                         const DT d = (DT)T::round(qs[s][j][k] * l1[s]);
                         DT* r = dwave + ((s * kFastJ + j) * bpw + bw) * ROW;
                         r[c] = d;
-                        if constexpr (kSign) r[L + c] = -d;
+                        r[L + c] = -d;
                     }
                 }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -402,6 +396,8 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
         constexpr int KSH = T::dt == kBF16 ? 16 : 0;
         uint32_t tb[S][kV];
         int jsel[S][NSUBL];
+        uint32_t yws[S][8], cws[S][4];   // per scheme: output pairs and byte codes
+        float errs[S];
         bool slow[S];
         float rl1v[S];
 #pragma unroll
@@ -485,10 +481,6 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
                     }
                 }
             }
-        }
-
-        int sstar = 0;
-        if constexpr (kSign) {
             // The selected candidate's level-word bytes (level times the entry size) of 4
             // elements in one register (v_perm_b32 picks byte j of two words at a time), and
             // the signs of x as byte masks (v_perm selectors 8-11 replicate bits 15, 31, 47
@@ -499,36 +491,36 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
             uint32_t pb[4], xm[4];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const uint32_t j = (uint32_t)jsel[0][(4 * g) / SUBN];
+                const uint32_t j = (uint32_t)jsel[s][(4 * g) / SUBN];
                 const uint32_t sel = j | ((j + 4u) << 8) | 0x0c0c0000u;   // byte j of the low word, then of the high word
-                const uint32_t lo = __builtin_amdgcn_perm(ent[0][4 * g + 1], ent[0][4 * g], sel);
-                const uint32_t hi = __builtin_amdgcn_perm(ent[0][4 * g + 3], ent[0][4 * g + 2], sel);
+                const uint32_t lo = __builtin_amdgcn_perm(ent[s][4 * g + 1], ent[s][4 * g], sel);
+                const uint32_t hi = __builtin_amdgcn_perm(ent[s][4 * g + 3], ent[s][4 * g + 2], sel);
                 pb[g] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
                 xm[g] = __builtin_amdgcn_perm(w[2 * g + 1], w[2 * g], 0x0b0a0908u);
             }
             // The output keeps the sign of x unless u = R_T(t / l2_j) is 0 (then +0 and a
             // positive code), which needs t < z_j: a quotient below T's normal range, which
             // the check above flags (x = +-0 included).
-            if (slow[0]) {
+            if (slow[s]) {
 #pragma unroll
                 for (int i = 0; i < kV; ++i) {
-                    const int j = jsel[0][i / SUBN];
-                    float zz = z[0][0];
+                    const int j = jsel[s][i / SUBN];
+                    float zz = z[s][0];
 #pragma unroll
-                    for (int jj = 1; jj < kFastJ; ++jj) zz = j == jj ? z[0][jj] : zz;
+                    for (int jj = 1; jj < kFastJ; ++jj) zz = j == jj ? z[s][jj] : zz;
                     // recomputed, not taken from the keys above: those die after the table index
                     uint32_t wv = w[i / 2];
                     asm("" : "+v"(wv));
                     const float a = fabsf(T::load((typename T::storage)(wv >> (16 * (i % 2)))));
-                    const float q = a * rl1v[0];
-                    const float t = q < tiny ? T::round(a / l1[0]) : T::round(q);
+                    const float q = a * rl1v[s];
+                    const float t = q < tiny ? T::round(a / l1[s]) : T::round(q);
                     if (!(key_of<T>(t) >= key_of<T>(zz))) xm[i / 4] &= ~(0xffu << (8 * (i % 4)));
                 }
             }
             // signed magnitudes: row of the selected candidate, byte offset plus L * ES if negative
             const char* rsel[NSUBL];
 #pragma unroll
-            for (int sb = 0; sb < NSUBL; ++sb) rsel[sb] = drow0 + (jsel[0][sb] * bpw) * ROW * ES;
+            for (int sb = 0; sb < NSUBL; ++sb) rsel[sb] = drow0 + ((s * kFastJ + jsel[s][sb]) * bpw) * ROW * ES;
             uint32_t ps[4];
 #pragma unroll
             for (int g = 0; g < 4; ++g) ps[g] = (xm[g] & kNeg) | pb[g];
@@ -536,96 +528,65 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
 #pragma unroll
             for (int i = 0; i < kV; ++i)
                 m[i] = *reinterpret_cast<const DT*>(rsel[i / SUBN] + ((ps[i / 4] >> (8 * (i % 4))) & 0xffu));
-            uint32_t yw[8];
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                if constexpr (T::dt == kBF16)   // the high halves: the values are bf16 already
-                    yw[k] = __builtin_amdgcn_perm(f2bits((float)m[2 * k + 1]), f2bits((float)m[2 * k]), 0x07060302u);
-                else
-                    yw[k] = (uint32_t)__builtin_bit_cast(uint16_t, m[2 * k]) |
-                            ((uint32_t)__builtin_bit_cast(uint16_t, m[2 * k + 1]) << 16);
+                if constexpr (T::dt == kBF16) {   // the high halves: the values are bf16 already
+                    yws[s][k] = __builtin_amdgcn_perm(f2bits((float)m[2 * k + 1]), f2bits((float)m[2 * k]), 0x07060302u);
+                } else {
+                    yws[s][k] = __builtin_bit_cast(uint32_t, (h2_t){(_Float16)m[2 * k], (_Float16)m[2 * k + 1]});
+                }
             }
-            if (valid) {
-                u32x4_t* q = reinterpret_cast<u32x4_t*>(y + off);
-                __builtin_nontemporal_store((u32x4_t){yw[0], yw[1], yw[2], yw[3]}, q);
-                __builtin_nontemporal_store((u32x4_t){yw[4], yw[5], yw[6], yw[7]}, q + 1);
-                if (codes) {   // byte codes: level | sign << (M + 2)
-                    uint32_t cw[4];
+            // byte codes: level | sign << (M + 2)
 #pragma unroll
-                    for (int g = 0; g < 4; ++g) cw[g] = (pb[g] / (uint32_t)ES) | (xm[g] & kCodeSign);
-                    *reinterpret_cast<uint4*>(codes + off) = make_uint4(cw[0], cw[1], cw[2], cw[3]);
-                }
-            }
-        } else {
-            // the selected candidate of every scheme
-            float msel[S][kV];
-            uint32_t lsel[S][kV];
-    #pragma unroll
-            for (int s = 0; s < S; ++s)
-    #pragma unroll
-                for (int i = 0; i < kV; ++i) {
-                    const int j = jsel[s][i / SUBN];
-                    const uint32_t off8 = (ent[s][i] >> (8 * j)) & 0xffu;
-                    lsel[s][i] = off8 / sizeof(DT);
-                    const char* a = drow0 + ((s * kFastJ + j) * bpw) * ROW * sizeof(DT) + off8;
-                    msel[s][i] = (float)*reinterpret_cast<const DT*>(a);
-                }
+            for (int g = 0; g < 4; ++g) cws[s][g] = (pb[g] / (uint32_t)ES) | (xm[g] & kCodeSign);
             if constexpr (S == 2) {
-                float sq0[kV], sq1[kV];
-    #pragma unroll
+                // the scheme's block error: R_T(|x| - d) squared and rounded, summed over the
+                // block in torch's order (|m| = d: the sign never changes the square)
+                float sq[kV];
+#pragma unroll
                 for (int i = 0; i < kV; i += 2) {
-                    float a0, a1, b0, b1;
-                    round2<T>(xa[i] - msel[0][i], xa[i + 1] - msel[0][i + 1], a0, a1);
-                    round2<T>(a0 * a0, a1 * a1, sq0[i], sq0[i + 1]);
-                    round2<T>(xa[i] - msel[S - 1][i], xa[i + 1] - msel[S - 1][i + 1], b0, b1);
-                    round2<T>(b0 * b0, b1 * b1, sq1[i], sq1[i + 1]);
-                }
-                const float s0 = T::round(block_row_sum(sq0, li, lpb, lane_base));
-                const float s1 = T::round(block_row_sum(sq1, li, lpb, lane_base));
-                sstar = better(s1, s0) ? 1 : 0;
-            }
-
-            float out[kV];
-            uint32_t cout[kV];
-            uint32_t zsel[NSUBL];
-    #pragma unroll
-            for (int sb = 0; sb < NSUBL; ++sb) {
-                const int s = (S == 2 && sstar) ? S - 1 : 0;
-                const int j = jsel[s][sb];
-                float zz = z[s][0];
-    #pragma unroll
-                for (int jj = 1; jj < kFastJ; ++jj) zz = j == jj ? z[s][jj] : zz;
-                zsel[sb] = key_of<T>(zz);
-            }
-    #pragma unroll
-            for (int i = 0; i < kV; ++i) {
-                const bool s1 = S == 2 && sstar;
-                const uint32_t t = s1 ? tb[S - 1][i] : tb[0][i];
-                const bool neg = (f2bits(xv[i]) >> 31) && t >= zsel[i / SUBN];
-                const float m = s1 ? msel[S - 1][i] : msel[0][i];
-                out[i] = neg ? -m : m;
-                const uint32_t lev = s1 ? lsel[S - 1][i] : lsel[0][i];
-                cout[i] = lev | ((neg ? 1u : 0u) << (M + 2));
-            }
-            if (valid) {
-                store16<T>(y + off, out);
-                if (codes) {
-                    if constexpr (M == 1) {
-                        uint32_t w0 = 0, w1 = 0;
-    #pragma unroll
-                        for (int i = 0; i < 8; ++i) {
-                            w0 |= (cout[i] & 0xfu) << (4 * i);
-                            w1 |= (cout[8 + i] & 0xfu) << (4 * i);
-                        }
-                        *reinterpret_cast<uint2*>(codes + off / 2) = make_uint2(w0, w1);
+                    if constexpr (T::dt == kF16) {
+                        // single correctly rounded fp16 ops, as in the candidate search
+                        const h2_t e = xp[i / 2] - __builtin_bit_cast(h2_t, yws[s][i / 2] & 0x7fff7fffu);
+                        h2_t q = e * e;
+                        asm("" : "+v"(q));
+                        sq[i] = (float)q.x;
+                        sq[i + 1] = (float)q.y;
                     } else {
-                        uint32_t cw[4];
-    #pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            cw[i] = (cout[4 * i] & 0xffu) | ((cout[4 * i + 1] & 0xffu) << 8) |
-                                    ((cout[4 * i + 2] & 0xffu) << 16) | ((cout[4 * i + 3] & 0xffu) << 24);
-                        *reinterpret_cast<uint4*>(codes + off) = make_uint4(cw[0], cw[1], cw[2], cw[3]);
+                        float e0, e1;
+                        round2<T>(xa[i] - fabsf((float)m[i]), xa[i + 1] - fabsf((float)m[i + 1]), e0, e1);
+                        round2<T>(e0 * e0, e1 * e1, sq[i], sq[i + 1]);
                     }
+                }
+                errs[s] = T::round(block_row_sum8(sq, li));
+            }
+        }
+
+        int sstar = 0;
+        // Mix: the scheme with the smaller block error (the first on a tie), the same
+        // value in the block's 8 lanes
+        if constexpr (S == 2) sstar = better(errs[1], errs[0]) ? 1 : 0;
+        uint32_t yw[8], cw[4];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) yw[k] = (S == 2 && sstar) ? yws[S - 1][k] : yws[0][k];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) cw[g] = (S == 2 && sstar) ? cws[S - 1][g] : cws[0][g];
+        if (valid) {
+            u32x4_t* q = reinterpret_cast<u32x4_t*>(y + off);
+            __builtin_nontemporal_store((u32x4_t){yw[0], yw[1], yw[2], yw[3]}, q);
+            __builtin_nontemporal_store((u32x4_t){yw[4], yw[5], yw[6], yw[7]}, q + 1);
+            if (codes) {
+                if constexpr (M == 1) {
+                    // 4-bit codes, element 2i in the low nibble of byte i: bytes 0 and 2 of
+                    // c | c >> 4 hold the nibble pairs of a word's 4 byte codes
+                    uint32_t t[4];
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) t[g] = cw[g] | (cw[g] >> 4);
+                    *reinterpret_cast<uint2*>(codes + off / 2) =
+                        make_uint2(__builtin_amdgcn_perm(t[1], t[0], 0x06040200u),
+                                   __builtin_amdgcn_perm(t[3], t[2], 0x06040200u));
+                } else {
+                    *reinterpret_cast<uint4*>(codes + off) = make_uint4(cw[0], cw[1], cw[2], cw[3]);
                 }
             }
         }
@@ -691,7 +652,7 @@ int launch_fast(const void* x, void* y, void* l1, void* l2i, void* sch, void* co
     constexpr int NTH = fast_threads<T>();
     using St = typename T::storage;
     const size_t lds = (size_t)S * (p.n + 2) * 4 +
-                       (size_t)(NTH >> lpb_log2) * S * kFastJ * fast_row<T, M, S>() * sizeof(DTabT<T>);
+                       (size_t)(NTH >> lpb_log2) * S * kFastJ * fast_row<T, M>() * sizeof(DTabT<T>);
     if (lds > 160 * 1024) return 0;
     if constexpr (SRC == kSrcX) {
         if (causal_t) return launch_fast<T, M, L2B, S, kSrcXCausal>(x, y, l1, l2i, sch, codes, nb, causal_t, slot, p, dev, st);

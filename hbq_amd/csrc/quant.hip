@@ -493,7 +493,8 @@ __global__ __launch_bounds__(kThreads) void causal_softmax_kernel(const typename
 
 extern "C" {
 
-// Test hook: 1 routes every HBQ and MXFP / NVFP call to the generic kernels (so both can be checked).
+// Test hook: 1 routes every HBQ and MXFP / NVFP call to the generic kernels (so both can be
+// checked); 2 makes a call that the table kernel declines fail instead of falling back.
 int hbq_set_generic_only(int on) {
     int old = g_hbq_force_generic;
     g_hbq_force_generic = on;
@@ -529,10 +530,11 @@ int hbq_mxfp_qdq(const void* x, void* y, void* scales, void* codes, int64_t rows
     p.tscale = round_host(tensor_scale, dtype);
     p.fused = compiled != 0;
     hipStream_t st = (hipStream_t)stream;
-    if (!g_hbq_force_generic) {
+    if (g_hbq_force_generic != 1) {
         const int fr = hbq_mx_fast_try(x, y, scales, codes, rows, cols, dtype, block_size, mbit, p, st);
         if (fr < 0) return -fr;
         if (fr == 1) return hbq_check_launch("hbq_mxfp_qdq");
+        if (g_hbq_force_generic == 2) return hbq_fail(HBQ_ERR_UNSUPPORTED, "the table kernel declined this call");
     }
     int rc;
     if (dtype == kF16) rc = dispatch_mx_m<F16>(mbit, g, x, y, scales, codes, cols, block_size, p, st);
@@ -582,11 +584,12 @@ int hbq_hbq_qdq(const void* x, void* y, void* l1_scale, void* l2_index, void* sc
     p.fused = compiled != 0;
     if (g.nb == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
-    if (!g_hbq_force_generic) {
+    if (g_hbq_force_generic != 1) {
         int fr = hbq_fast_try(x, y, l1_scale, l2_index, scheme, codes, rows, cols, dtype, block_size, mbit,
                               l2_block_size, l2_sc_bit, l2_scheme, p, st);
         if (fr < 0) return -fr;
         if (fr == 1) return hbq_check_launch("hbq_hbq_qdq");
+        if (g_hbq_force_generic == 2) return hbq_fail(HBQ_ERR_UNSUPPORTED, "the table kernel declined this call");
     }
     int rc;
     if (dtype == kF16) rc = dispatch_hbq<F16>(mbit, S, l2_block_size, g, x, y, l1_scale, l2_index, scheme, codes, cols, block_size, p, st);
@@ -612,7 +615,7 @@ int hbq_hbq_qdq_causal(void* x, int64_t mats, int64_t t, int dtype, int block_si
         return rc;
     p.fused = compiled != 0;
     if (g.nb == 0) return 0;
-    const int fr = g_hbq_force_generic ? 0
+    const int fr = g_hbq_force_generic == 1 ? 0
                                        : hbq_fast_try(x, x, nullptr, nullptr, nullptr, nullptr, mats * t, t, dtype,
                                                       block_size, mbit, l2_block_size, l2_sc_bit, l2_scheme, p,
                                                       (hipStream_t)stream, t);

@@ -256,4 +256,42 @@ __device__ __forceinline__ float block_row_sum(const float* sq, int li, int lpb,
     return ((P[0] + P[1]) + P[2]) + P[3];
 }
 
+// block_row_sum for blocks of 8 lanes (the table kernels' layout; blocks start at a
+// multiple of 8 lanes): the same additions in the same order, with DPP moves in
+// place of the lane shuffles
+template <int CTRL>
+__device__ __forceinline__ float dpp_movf(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float block_row_sum8(const float* sq, int li) {
+    float run[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int step = 0; step < 4; ++step) {
+        float prev[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) prev[k] = dpp_movf<0x111>(run[k]);   // row_shr:1, lane - 1
+        if ((li & 3) == step) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                float a = step == 0 ? 0.f : prev[k];
+                a += sq[k];
+                a += sq[k + 4];
+                a += sq[k + 8];
+                a += sq[k + 12];
+                run[k] = a;
+            }
+        }
+    }
+    float P[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        // quad_perm [3,3,3,3]: lanes 0-3 of the block hold lane 3's cascade, 4-7 lane 7's;
+        // row_half_mirror (lane i from lane 7 - i) brings the other one: the two-term sum
+        // is the same in every lane since a + b == b + a
+        const float q = dpp_movf<0xff>(run[k]);
+        P[k] = q + dpp_movf<0x141>(q);
+    }
+    return ((P[0] + P[1]) + P[2]) + P[3];
+}
+
 }  // namespace hbq

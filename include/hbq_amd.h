@@ -63,9 +63,11 @@ const char *hbq_last_error(void);
 /* ABI revision of this header (2: the `compiled` element-rounding argument). */
 int hbq_abi_version(void);
 
-/* No reference counterpart: a test hook.  on != 0 routes every hbq_hbq_qdq and
+/* No reference counterpart: a test hook.  on == 1 routes every hbq_hbq_qdq and
  * hbq_mxfp_qdq call to the generic kernels instead of the table-driven ones;
- * returns the old setting. */
+ * on == 2 makes a call that the table-driven kernel declines fail with
+ * HBQ_ERR_UNSUPPORTED instead of falling back to the generic one; 0 restores the
+ * default.  Returns the old setting. */
 int hbq_set_generic_only(int on);
 
 /*

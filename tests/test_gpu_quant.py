@@ -25,10 +25,28 @@ HBQCFG = {
     "hbq_kv4": dict(ebit=2, mbit=1, l2_block_size=8, l2_sc_bit=2, l2_scheme="SIG-1"),
     "hbq_a_wgt_ceil": dict(ebit=2, mbit=1, l2_block_size=8, l2_sc_bit=2, l2_scheme="Mix", use_ceil=True),
     "hbq_pot": dict(ebit=2, mbit=1, l2_block_size=4, l2_sc_bit=1, l2_scheme="PoT"),
-    # no reference fixtures for these two: checked against the oracle and the generic kernel
+    # no reference fixtures for these: checked against the oracle and the generic kernel
     "hbq_m3": dict(ebit=2, mbit=3, l2_block_size=8, l2_sc_bit=2, l2_scheme="SIG-1"),
     "hbq_l16": dict(ebit=2, mbit=2, l2_block_size=16, l2_sc_bit=2, l2_scheme="FP-1"),
+    # two-scheme (Mix) tables at 3 and 2 mantissa bits: the largest magnitude rows in LDS
+    "hbq_m3_mix": dict(ebit=2, mbit=3, l2_block_size=16, l2_sc_bit=2, l2_scheme="Mix"),
+    "hbq_m2_mix": dict(ebit=2, mbit=2, l2_block_size=32, l2_sc_bit=2, l2_scheme="Mix"),
 }
+NO_FIXTURES = ("hbq_m3", "hbq_l16", "hbq_m3_mix", "hbq_m2_mix")
+
+
+def _table_and_generic(q, x):
+    """q.quantize(x) on the table-driven kernel (a call that it declines fails instead of
+    falling back) and on the generic kernel."""
+    from hbq_amd import _lib
+    old = _lib.lib().hbq_set_generic_only(2)
+    try:
+        fast = q.quantize(x)
+        _lib.lib().hbq_set_generic_only(1)
+        gen = q.quantize(x)
+    finally:
+        _lib.lib().hbq_set_generic_only(old)
+    return fast, gen
 
 
 def _mx(kw, **extra):
@@ -107,7 +125,7 @@ def test_mxfp_bf16_raises(gpu):
         _mx(MXCFG["mxfp4"]).q(torch.zeros(4, 32, dtype=torch.bfloat16, device=gpu))
 
 
-@pytest.mark.parametrize("name", [n for n in HBQCFG if n not in ("hbq_m3", "hbq_l16")])
+@pytest.mark.parametrize("name", [n for n in HBQCFG if n not in NO_FIXTURES])
 @pytest.mark.parametrize("inp", ["f16", "f16w", "bf16"])
 @pytest.mark.parametrize("uqk", [False, True])
 def test_hbq_golden(gpu, golden_hbq, golden_extra, golden_compiled, name, inp, uqk):
@@ -278,21 +296,15 @@ def test_hbq_3d_input(gpu, oracle):
 
 
 @pytest.mark.parametrize("name", ["hbq_a_act", "hbq_a_wgt", "hbq_e_act", "hbq_e_wgt", "hbq_kv4", "hbq_a_wgt_ceil",
-                                  "hbq_m3", "hbq_l16"])
+                                  "hbq_m3", "hbq_l16", "hbq_m3_mix", "hbq_m2_mix"])
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("uqk", [True, False])
 def test_hbq_table_kernel_equals_generic(gpu, name, dt, uqk):
     """The table-driven kernel and the generic kernel agree bit for bit, codes and scales included."""
-    from hbq_amd import _lib
     print(f"fast vs generic {name} {dt} use_quant_kernel={uqk}", flush=True)
     x = _edge_rows(synth(512, 4096, 17, dt)).to(gpu)
     q = _hbq(HBQCFG[name], use_quant_kernel=uqk)
-    fast = q.quantize(x)
-    old = _lib.lib().hbq_set_generic_only(1)
-    try:
-        gen = q.quantize(x)
-    finally:
-        _lib.lib().hbq_set_generic_only(old)
+    fast, gen = _table_and_generic(q, x)
     assert mismatches(to_bits(fast.y), to_bits(gen.y), dt) == 0
     ok = ~torch.isnan(fast.y)          # codes of NaN outputs are unspecified
     per_byte = ok if q.mbit != 1 else ok.view(ok.shape[0], -1, 2).all(-1)
@@ -312,19 +324,13 @@ def test_mxfp_table_kernel_equals_generic(gpu, name, dyn):
     """The table-driven MXFP / NVFP kernel (fp16, whole blocks) and the generic kernel agree
     bit for bit on outputs, codes and scales, edge rows (zeros, +-inf, NaN, huge, subnormal,
     quotients in the fp16 subnormal range) included."""
-    from hbq_amd import _lib
     print(f"mx fast vs generic {name} activate_dynamo={dyn}", flush=True)
     x = _edge_rows(synth(512, 4096, 18, "f16"))
     x[6] = x[6] * 1e-3            # blocks whose quotients reach the fp16 subnormal range
     x[7, ::3] = 0.0
     xg = x.to(gpu)
     q = _mx(MXFAST[name], activate_dynamo=dyn)
-    fast = q.quantize(xg)
-    old = _lib.lib().hbq_set_generic_only(1)
-    try:
-        gen = q.quantize(xg)
-    finally:
-        _lib.lib().hbq_set_generic_only(old)
+    fast, gen = _table_and_generic(q, xg)
     assert mismatches(to_bits(fast.y), to_bits(gen.y), "f16") == 0
     assert torch.equal(fast.codes, gen.codes)
     assert mismatches(to_bits(fast.scales), to_bits(gen.scales), "f16") == 0
@@ -349,7 +355,6 @@ def test_mxfp_table_kernel_partial_tiles(gpu, oracle, name, shape):
 def test_hbq_causal_zero_blocks(gpu, oracle, name):
     """Attention-weight-like input (row i zero past column i): waves whose eight blocks are all
     zero take the table kernel's zero path; everything equals the oracle and the generic kernel."""
-    from hbq_amd import _lib
     print(f"hbq causal zeros {name}", flush=True)
     T = 2048
     g = torch.Generator().manual_seed(23)
@@ -363,12 +368,7 @@ def test_hbq_causal_zero_blocks(gpu, oracle, name):
     assert mismatches(to_bits(q.shared_scale), ref["l1"], "f16") == 0
     assert np.array_equal(q.l2_scale.cpu().numpy(), ref["l2idx"].astype(np.int64))
     assert np.array_equal(q.blk_l2_scheme.cpu().numpy(), ref["scheme"].astype(np.int64))
-    fast = q.quantize(x.to(gpu))
-    old = _lib.lib().hbq_set_generic_only(1)
-    try:
-        gen = q.quantize(x.to(gpu))
-    finally:
-        _lib.lib().hbq_set_generic_only(old)
+    fast, gen = _table_and_generic(q, x.to(gpu))
     assert torch.equal(fast.codes, gen.codes)
 
 
