@@ -34,13 +34,14 @@ namespace hbq {
 constexpr int kLutSlots = 16;
 constexpr int kLutMaxBinades = 12;
 constexpr int kLutMaxEntries = 2 * (kLutMaxBinades * 1024 + 2);
+static_assert(kLutMaxEntries % 4 == 0, "the table copy reads whole 16-byte pieces of a slot row");
 constexpr int kFastJ = 4;
 
 // level tables: per slot, S schemes of (n + 2) words: [0] below the table range
 // (all levels 0), [1 .. n] the binades [2^lo, 2^hi), [n + 1] at or above 2^hi
 // (saturated).  Byte j of a word is candidate j's level times the element size
 // of the magnitude table, i.e. its byte offset in a table row.
-static __device__ uint32_t g_lut[kLutSlots][kLutMaxEntries];
+static __device__ __attribute__((aligned(16))) uint32_t g_lut[kLutSlots][kLutMaxEntries];
 // per slot: z[s][j] = smallest t > 0 with R_T(t / l2[j][s]) != 0
 static __device__ float g_lut_z[kLutSlots][2 * kFastJ];
 // per slot: R_T(level value * l2[j][s]) for every level (block independent)
@@ -195,15 +196,32 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
     constexpr int SUBN = L2B <= kV ? L2B : kV;
     constexpr int NTH = fast_threads<T>();
     constexpr int blocks_per_wg = NTH / lpb;
-    extern __shared__ uint32_t smem[];
+    extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
     const int per = p.n + 2;
     uint32_t* lut = smem;
-
-    for (int i = threadIdx.x; i < S * per; i += NTH) lut[i] = g_lut[slot][i];
     const int li = (int)(threadIdx.x & (lpb - 1));
     const int lane = (int)(threadIdx.x & 63);
     const int lane_base = lane - li;
     const int bw = lane / lpb;
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+    // The level table goes to LDS in 16-byte pieces, every global load issued before the
+    // first LDS store (a loop with a run-time count waits for each load in turn); the
+    // first tile's input loads follow them, so one memory latency covers both.  The
+    // slot rows are 16-byte aligned; the up to 3 words copied past the table land in
+    // the magnitude rows, which every tile writes before reading.
+    constexpr int kCopyWords = S * (kLutMaxBinades * (T::dt == kF16 ? 1024 : 128) + 2);
+    constexpr int kCopy = ((kCopyWords + 3) / 4 + NTH - 1) / NTH;
+    const int nw4 = (S * per + 3) / 4;
+    u32x4_t cp[kCopy];
+    {
+        const u32x4_t* src4 = reinterpret_cast<const u32x4_t*>(g_lut[slot]);
+#pragma unroll
+        for (int c = 0; c < kCopy; ++c) {
+            const int i = (int)threadIdx.x + c * NTH;
+            cp[c] = src4[i < nw4 ? i : nw4 - 1];
+        }
+    }
 
     float z[S][kFastJ];
     // this lane builds levels c = li and li + 8 (L = 16) of every (scheme, candidate) row
@@ -217,7 +235,6 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
 #pragma unroll
             for (int k = 0; k < CPL; ++k) qs[s][j][k] = g_lut_qs[slot][s][j][(li + k * lpb) & 31];
         }
-    __syncthreads();
 
     // this lane's row (s, j) starts at dwave + ((s*J + j)*bpw + bw) * ROW; table words hold byte offsets into it
     DT* dwave = reinterpret_cast<DT*>(smem + S * per) + (threadIdx.x >> 6) * (S * kFastJ * bpw * ROW);
@@ -244,17 +261,29 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
     // last tile reads its current block again and the data is replaced by zeros), and no
     // other path writes their registers, so the compiler waits for them only where the next
     // tile reads them; after the wave's last tile none are issued (a wave-uniform branch).
-    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
     constexpr bool kPrefetch = SRC == kSrcX;
     u32x4_t pf0 = {0u, 0u, 0u, 0u}, pf1 = {0u, 0u, 0u, 0u};
-    auto prefetch = [&](int64_t t, int64_t g_cur) __attribute__((always_inline)) {
-        if (t >= nwork) return;
+    auto prefetch_load = [&](int64_t t, int64_t g_cur) __attribute__((always_inline)) {
         const int64_t g = t * blocks_per_wg + (threadIdx.x / lpb);
         const u32x4_t* q = reinterpret_cast<const u32x4_t*>(x + (g < nb ? g : g_cur) * (int64_t)block + (int64_t)li * kV);
         pf0 = __builtin_nontemporal_load(q);
         pf1 = __builtin_nontemporal_load(q + 1);
     };
-    if constexpr (kPrefetch) prefetch(first, 0);
+    auto prefetch = [&](int64_t t, int64_t g_cur) __attribute__((always_inline)) {
+        if (t >= nwork) return;
+        prefetch_load(t, g_cur);
+    };
+    // the grid never exceeds the tiles, so first < nwork: no branch around these loads
+    if constexpr (kPrefetch) prefetch_load(first, 0);
+    {
+        u32x4_t* dst4 = reinterpret_cast<u32x4_t*>(lut);
+#pragma unroll
+        for (int c = 0; c < kCopy; ++c) {
+            const int i = (int)threadIdx.x + c * NTH;
+            if (i < nw4) dst4[i] = cp[c];
+        }
+    }
+    __syncthreads();
 
     for (int64_t tile = first; tile < nwork; tile += stride) {
         int64_t gb;
