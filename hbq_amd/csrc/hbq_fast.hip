@@ -158,9 +158,11 @@ __global__ void build_lut_kernel(int slot, FastParams p) {
 
 // Workgroup size: the fp16 level table (1024 words a binade) takes 37 KB of LDS,
 // which 256-thread workgroups would replicate down to 3 waves a SIMD; 512 threads
-// share one copy between 8 waves.  The bf16 table is 8 times smaller.
-template <class T>
-constexpr int fast_threads() { return T::dt == kF16 ? 512 : 256; }
+// share one copy between 8 waves.  The two tables of the fp16 two-scheme (Mix) E2M1
+// kernel take 57 KB: 1024 threads (121 KB of LDS with the magnitude rows, at most 128
+// VGPRs) run 4 waves a SIMD where 512 would run 2.  The bf16 table is 8 times smaller.
+template <class T, int M, int S>
+constexpr int fast_threads() { return T::dt == kF16 ? (S == 2 && M == 1 ? 1024 : 512) : 256; }
 
 // Per-block magnitude rows.  The negated magnitudes fill the second half of each
 // row: a level-word byte (level times the entry size) plus L * sizeof(DT) addresses
@@ -178,7 +180,7 @@ constexpr int kSrcXCausal = 3;
 // Block 128 (8 lanes x 16 elements).  Per-wave magnitude tables, laid out
 // [scheme][candidate][block-in-wave][row of fast_row() entries].
 template <class T, int M, int L2B, int S, int SRC = kSrcX>
-__global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typename T::storage* __restrict__ x,
+__global__ __launch_bounds__((fast_threads<T, M, S>())) void hbq_fast_kernel(const typename T::storage* __restrict__ x,
                                                             typename T::storage* __restrict__ y,
                                                             typename T::storage* __restrict__ l1_out,
                                                             uint8_t* __restrict__ l2i_out,
@@ -194,7 +196,7 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
     constexpr int NSUBL = L2B <= kV ? kV / L2B : 1;
     constexpr int LPS = L2B <= kV ? 1 : L2B / kV;
     constexpr int SUBN = L2B <= kV ? L2B : kV;
-    constexpr int NTH = fast_threads<T>();
+    constexpr int NTH = fast_threads<T, M, S>();
     constexpr int blocks_per_wg = NTH / lpb;
     extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
     const int per = p.n + 2;
@@ -224,20 +226,22 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
     }
 
     float z[S][kFastJ];
-    // this lane builds levels c = li and li + 8 (L = 16) of every (scheme, candidate) row
-    constexpr int CPL = (L + lpb - 1) / lpb;
-    float qs[S][kFastJ][CPL];
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
-        for (int j = 0; j < kFastJ; ++j) {
-            z[s][j] = g_lut_z[slot][s * kFastJ + j];
-#pragma unroll
-            for (int k = 0; k < CPL; ++k) qs[s][j][k] = g_lut_qs[slot][s][j][(li + k * lpb) & 31];
-        }
+        for (int j = 0; j < kFastJ; ++j) z[s][j] = g_lut_z[slot][s * kFastJ + j];
+    // this lane builds levels c = li and li + 8 (L = 16) of every (scheme, candidate) row
+    // from R_T(level * l2_j), kept in LDS after the level table as [li][s][j][k] (a lane's
+    // values contiguous) and read back for each tile: in registers they would hold
+    // S * 4 * CPL VGPRs for the whole kernel
+    constexpr int CPL = (L + lpb - 1) / lpb;
+    constexpr int QSL = S * kFastJ * CPL;   // floats of one lane
+    float* const qsl = reinterpret_cast<float*>(smem + (S * per + 3) / 4 * 4);
+    const float qsv = g_lut_qs[slot][(threadIdx.x / (kFastJ * CPL)) % S][(threadIdx.x / CPL) % kFastJ]
+                              [((threadIdx.x / QSL) % lpb + (threadIdx.x % CPL) * lpb) & 31];
 
     // this lane's row (s, j) starts at dwave + ((s*J + j)*bpw + bw) * ROW; table words hold byte offsets into it
-    DT* dwave = reinterpret_cast<DT*>(smem + S * per) + (threadIdx.x >> 6) * (S * kFastJ * bpw * ROW);
+    DT* dwave = reinterpret_cast<DT*>(qsl + lpb * QSL) + (threadIdx.x >> 6) * (S * kFastJ * bpw * ROW);
     const char* drow0 = reinterpret_cast<const char*>(dwave + bw * ROW);
     const int64_t ntiles = (nb + blocks_per_wg - 1) / blocks_per_wg;
     const float tiny = T::dt == kF16 ? 6.103515625e-05f : 1.17549435e-38f;
@@ -283,6 +287,7 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
             if (i < nw4) dst4[i] = cp[c];
         }
     }
+    if (threadIdx.x < lpb * QSL) qsl[threadIdx.x] = qsv;
     __syncthreads();
 
     for (int64_t tile = first; tile < nwork; tile += stride) {
@@ -396,6 +401,13 @@ __global__ __launch_bounds__(fast_threads<T>()) void hbq_fast_kernel(const typen
         }
 
         // magnitudes R_T(R_T(level * l2_j) * l1_s) of this block
+        float qs[S][kFastJ][CPL];
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int j = 0; j < kFastJ; ++j)
+#pragma unroll
+                for (int k = 0; k < CPL; ++k) qs[s][j][k] = qsl[li * QSL + (s * kFastJ + j) * CPL + k];
 #pragma unroll
         for (int s = 0; s < S; ++s)
 #pragma unroll
@@ -678,9 +690,10 @@ template <class T, int M, int L2B, int S, int SRC = kSrcX>
 int launch_fast(const void* x, void* y, void* l1, void* l2i, void* sch, void* codes, int64_t nb, int64_t causal_t,
                 int slot, const FastParams& p, int dev, hipStream_t st, const FastSrc& src = FastSrc{}, int64_t cols = 0) {
     constexpr int lpb_log2 = 3;
-    constexpr int NTH = fast_threads<T>();
+    constexpr int NTH = fast_threads<T, M, S>();
     using St = typename T::storage;
-    const size_t lds = (size_t)S * (p.n + 2) * 4 +
+    constexpr int CPL = ((1 << (M + 2)) + 7) / 8;
+    const size_t lds = (size_t)(S * (p.n + 2) + 3) / 4 * 16 + (size_t)8 * S * kFastJ * CPL * 4 +
                        (size_t)(NTH >> lpb_log2) * S * kFastJ * fast_row<T, M>() * sizeof(DTabT<T>);
     if (lds > 160 * 1024) return 0;
     if constexpr (SRC == kSrcX) {
