@@ -164,6 +164,14 @@ __global__ void build_lut_kernel(int slot, FastParams p) {
 template <class T, int M, int S>
 constexpr int fast_threads() { return T::dt == kF16 ? (S == 2 && M == 1 ? 1024 : 512) : 256; }
 
+// The bf16 two-scheme memory-input kernels run 4 waves a SIMD (128 VGPRs) without the
+// input prefetch, whose 8 registers would take them to 3: 12-13% faster than 3 waves
+// with it.  The others take what their registers give (a minimum of 1 places no bound).
+template <class T, int S>
+constexpr bool fast_prefetch() { return !(S == 2 && T::dt == kBF16); }
+template <class T, int S, int SRC>
+constexpr int fast_min_waves() { return SRC == kSrcX && !fast_prefetch<T, S>() ? 4 : 1; }
+
 // Per-block magnitude rows.  The negated magnitudes fill the second half of each
 // row: a level-word byte (level times the entry size) plus L * sizeof(DT) addresses
 // -d, so one LDS read of the selected candidate returns the signed output.  Rows are
@@ -180,7 +188,8 @@ constexpr int kSrcXCausal = 3;
 // Block 128 (8 lanes x 16 elements).  Per-wave magnitude tables, laid out
 // [scheme][candidate][block-in-wave][row of fast_row() entries].
 template <class T, int M, int L2B, int S, int SRC = kSrcX>
-__global__ __launch_bounds__((fast_threads<T, M, S>())) void hbq_fast_kernel(const typename T::storage* __restrict__ x,
+__global__ __launch_bounds__((fast_threads<T, M, S>())) __attribute__((amdgpu_waves_per_eu(fast_min_waves<T, S, SRC>())))
+void hbq_fast_kernel(const typename T::storage* __restrict__ x,
                                                             typename T::storage* __restrict__ y,
                                                             typename T::storage* __restrict__ l1_out,
                                                             uint8_t* __restrict__ l2i_out,
@@ -265,7 +274,7 @@ __global__ __launch_bounds__((fast_threads<T, M, S>())) void hbq_fast_kernel(con
     // last tile reads its current block again and the data is replaced by zeros), and no
     // other path writes their registers, so the compiler waits for them only where the next
     // tile reads them; after the wave's last tile none are issued (a wave-uniform branch).
-    constexpr bool kPrefetch = SRC == kSrcX;
+    constexpr bool kPrefetch = SRC == kSrcX && fast_prefetch<T, S>();
     u32x4_t pf0 = {0u, 0u, 0u, 0u}, pf1 = {0u, 0u, 0u, 0u};
     auto prefetch_load = [&](int64_t t, int64_t g_cur) __attribute__((always_inline)) {
         const int64_t g = t * blocks_per_wg + (threadIdx.x / lpb);
