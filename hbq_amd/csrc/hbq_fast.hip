@@ -240,17 +240,32 @@ void hbq_fast_kernel(const typename T::storage* __restrict__ x,
 #pragma unroll
         for (int j = 0; j < kFastJ; ++j) z[s][j] = g_lut_z[slot][s * kFastJ + j];
     // this lane builds levels c = li and li + 8 (L = 16) of every (scheme, candidate) row
-    // from R_T(level * l2_j), kept in LDS after the level table as [li][s][j][k] (a lane's
-    // values contiguous) and read back for each tile: in registers they would hold
-    // S * 4 * CPL VGPRs for the whole kernel
+    // from R_T(level * l2_j).  The two-scheme kernels keep them in LDS after the level
+    // table as [li][s][j][k] (a lane's values contiguous) and read them back for each
+    // tile, since in registers they would hold 8 * CPL VGPRs for the whole kernel; the
+    // one-scheme kernels, whose occupancy does not depend on them, keep them in
+    // registers (1-2% faster)
     constexpr int CPL = (L + lpb - 1) / lpb;
     constexpr int QSL = S * kFastJ * CPL;   // floats of one lane
+    constexpr bool kQsLds = S == 2;
     float* const qsl = reinterpret_cast<float*>(smem + (S * per + 3) / 4 * 4);
-    const float qsv = g_lut_qs[slot][(threadIdx.x / (kFastJ * CPL)) % S][(threadIdx.x / CPL) % kFastJ]
-                              [((threadIdx.x / QSL) % lpb + (threadIdx.x % CPL) * lpb) & 31];
+    float qsv = 0.f;
+    float qreg[S][kFastJ][CPL];
+    if constexpr (kQsLds) {
+        qsv = g_lut_qs[slot][(threadIdx.x / (kFastJ * CPL)) % S][(threadIdx.x / CPL) % kFastJ]
+                      [((threadIdx.x / QSL) % lpb + (threadIdx.x % CPL) * lpb) & 31];
+    } else {
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int j = 0; j < kFastJ; ++j)
+#pragma unroll
+                for (int k = 0; k < CPL; ++k) qreg[s][j][k] = g_lut_qs[slot][s][j][(li + k * lpb) & 31];
+    }
 
     // this lane's row (s, j) starts at dwave + ((s*J + j)*bpw + bw) * ROW; table words hold byte offsets into it
-    DT* dwave = reinterpret_cast<DT*>(qsl + lpb * QSL) + (threadIdx.x >> 6) * (S * kFastJ * bpw * ROW);
+    DT* dwave = reinterpret_cast<DT*>(kQsLds ? qsl + lpb * QSL : reinterpret_cast<float*>(smem + S * per)) +
+                (threadIdx.x >> 6) * (S * kFastJ * bpw * ROW);
     const char* drow0 = reinterpret_cast<const char*>(dwave + bw * ROW);
     const int64_t ntiles = (nb + blocks_per_wg - 1) / blocks_per_wg;
     const float tiny = T::dt == kF16 ? 6.103515625e-05f : 1.17549435e-38f;
@@ -296,7 +311,7 @@ void hbq_fast_kernel(const typename T::storage* __restrict__ x,
             if (i < nw4) dst4[i] = cp[c];
         }
     }
-    if (threadIdx.x < lpb * QSL) qsl[threadIdx.x] = qsv;
+    if (kQsLds && threadIdx.x < lpb * QSL) qsl[threadIdx.x] = qsv;
     __syncthreads();
 
     for (int64_t tile = first; tile < nwork; tile += stride) {
@@ -416,7 +431,7 @@ void hbq_fast_kernel(const typename T::storage* __restrict__ x,
 #pragma unroll
             for (int j = 0; j < kFastJ; ++j)
 #pragma unroll
-                for (int k = 0; k < CPL; ++k) qs[s][j][k] = qsl[li * QSL + (s * kFastJ + j) * CPL + k];
+                for (int k = 0; k < CPL; ++k) qs[s][j][k] = kQsLds ? qsl[li * QSL + (s * kFastJ + j) * CPL + k] : qreg[s][j][k];
 #pragma unroll
         for (int s = 0; s < S; ++s)
 #pragma unroll
@@ -701,8 +716,9 @@ int launch_fast(const void* x, void* y, void* l1, void* l2i, void* sch, void* co
     constexpr int lpb_log2 = 3;
     constexpr int NTH = fast_threads<T, M, S>();
     using St = typename T::storage;
-    constexpr int CPL = ((1 << (M + 2)) + 7) / 8;
-    const size_t lds = (size_t)(S * (p.n + 2) + 3) / 4 * 16 + (size_t)8 * S * kFastJ * CPL * 4 +
+    constexpr int CPL = ((1 << (M + 2)) + 7) / 8;   // the level constants in LDS: two-scheme kernels
+    const size_t lds = (S == 2 ? (size_t)(S * (p.n + 2) + 3) / 4 * 16 + (size_t)8 * S * kFastJ * CPL * 4
+                               : (size_t)S * (p.n + 2) * 4) +
                        (size_t)(NTH >> lpb_log2) * S * kFastJ * fast_row<T, M>() * sizeof(DTabT<T>);
     if (lds > 160 * 1024) return 0;
     if constexpr (SRC == kSrcX) {
