@@ -351,6 +351,29 @@ def test_mxfp_table_kernel_partial_tiles(gpu, oracle, name, shape):
     assert mismatches(to_bits(out.scales), s, "f16") == 0
 
 
+@pytest.mark.parametrize("name", ["hbq_a_wgt", "hbq_e_wgt", "hbq_a_act"])
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("rows", [1, 37, 129])
+def test_hbq_table_kernel_partial_tiles(gpu, oracle, name, dt, rows):
+    """Block counts that leave the last workgroup tile partial (32 blocks a tile for bf16,
+    64 for fp16 one-scheme, 128 for the fp16 two-scheme kernel), on the table kernel only,
+    against the oracle: outputs, L1 scales, L2 indices and schemes."""
+    print(f"hbq partial tiles {name} {dt} rows={rows}", flush=True)
+    x = synth(rows, 4096, 24 + rows, dt)
+    q = _hbq(HBQCFG[name], keep_l2_scale=True)
+    from hbq_amd import _lib
+    old = _lib.lib().hbq_set_generic_only(2)
+    try:
+        y = q.q(x.to(gpu))
+    finally:
+        _lib.lib().hbq_set_generic_only(old)
+    ref = oracle.hbq_qdq(to_bits(x), dt, block_size=128, **HBQCFG[name])
+    assert mismatches(to_bits(y), ref["y"], dt) == 0
+    assert mismatches(to_bits(q.shared_scale), ref["l1"], dt) == 0
+    assert np.array_equal(q.l2_scale.cpu().numpy(), ref["l2idx"].astype(np.int64))
+    assert np.array_equal(q.blk_l2_scheme.cpu().numpy(), ref["scheme"].astype(np.int64))
+
+
 @pytest.mark.parametrize("name", ["hbq_a_act", "hbq_a_wgt", "hbq_kv4"])
 def test_hbq_causal_zero_blocks(gpu, oracle, name):
     """Attention-weight-like input (row i zero past column i): waves whose eight blocks are all
