@@ -172,13 +172,25 @@ __device__ __forceinline__ void fold_block_impl(const f16v& acc, h2_t* H) {
                     Mg[g] = __builtin_bit_cast(
                         float, (__builtin_bit_cast(uint32_t, mxg[g]) & 0x7f800000u) + (17u << 23) + 0x400000u);
                 if (__builtin_expect(!wave_any(top), 1)) {
+                    // all 16 magic adds, then all 16 exact subtractions, then the 8 paired
+                    // conversions: independent instructions back to back instead of one
+                    // add-subtract-convert chain per pair (which also waits a cycle before
+                    // each conversion); the barrier keeps the compiler from interleaving
+                    // them again or forming v_fma_mix
+                    float t[16];
 #pragma unroll
                     for (int g = 0; g < NG; ++g)
 #pragma unroll
-                        for (int r = g * RPG; r < (g + 1) * RPG; r += 2) {
-                            const float t0 = acc[r] + Mg[g], t1 = acc[r + 1] + Mg[g];
-                            H[r / 2] = H[r / 2] + sub_pair(t0, t1, Mg[g]);
-                        }
+                        for (int r = g * RPG; r < (g + 1) * RPG; ++r) t[r] = acc[r] + Mg[g];
+#pragma unroll
+                    for (int g = 0; g < NG; ++g)
+#pragma unroll
+                        for (int r = g * RPG; r < (g + 1) * RPG; ++r) t[r] = t[r] - Mg[g];
+                    asm("" : "+v"(t[0]), "+v"(t[1]), "+v"(t[2]), "+v"(t[3]), "+v"(t[4]), "+v"(t[5]), "+v"(t[6]),
+                        "+v"(t[7]), "+v"(t[8]), "+v"(t[9]), "+v"(t[10]), "+v"(t[11]), "+v"(t[12]), "+v"(t[13]),
+                        "+v"(t[14]), "+v"(t[15]));
+#pragma unroll
+                    for (int p = 0; p < 8; ++p) H[p] = H[p] + cvt2(t[2 * p], t[2 * p + 1]);
                 } else {
 #pragma unroll
                     for (int g = 0; g < NG; ++g) {
